@@ -1,0 +1,155 @@
+/*
+ * slo_attn.h -- C-ABI of the MI355X (gfx950) attention hot path for the
+ * SLO-aware nano-vLLM engine.
+ *
+ * All pointers are raw device pointers owned by the caller (PyTorch tensors in
+ * the Python host layer).  All entry points are asynchronous on `stream`
+ * (a hipStream_t), never synchronise the device, never allocate device memory
+ * and never abort: they return SLO_OK or an error code, and slo_last_error()
+ * describes the last failure on the calling thread.  Every launch has a grid
+ * sized from shapes and capacities only, so calls may be recorded into a HIP
+ * graph.
+ *
+ * Pool geometry (per layer), identical to the reference engine:
+ *   K/V   [num_blocks, block_size, num_kv_heads, head_dim]  bf16, or E4M3FN
+ *         bytes when kv_dtype == SLO_KV_FP8_E4M3FN
+ *   scale [num_blocks, block_size, num_kv_heads]            fp32 (FP8 only)
+ *   slot  = block_table[pos / block_size] * block_size + pos % block_size
+ */
+#ifndef SLO_ATTN_H_
+#define SLO_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* slo_stream_t; /* hipStream_t */
+
+enum {
+  SLO_OK = 0,
+  SLO_ERR_INVALID = 1,     /* bad argument, shape or stride */
+  SLO_ERR_HIP = 2,         /* a HIP runtime call failed */
+  SLO_ERR_WORKSPACE = 3,   /* workspace smaller than slo_attention_workspace_bytes */
+  SLO_ERR_UNSUPPORTED = 4  /* geometry this build does not implement */
+};
+
+enum { SLO_KV_BF16 = 0, SLO_KV_FP8_E4M3FN = 1 };
+
+enum { SLO_PHASE_DECODE = 1, SLO_PHASE_PREFILL = 2, SLO_PHASE_ALL = 3 };
+
+/* Smallest FP8 scale: a power of two, so a scale is always a normal fp32 and
+ * no denormal arithmetic can change a code. */
+#define SLO_FP8_SCALE_FLOOR 5.421010862427522e-20f /* 2^-64 */
+
+/*
+ * Slot-mapped KV-cache write, optionally quantising to E4M3FN.
+ *
+ * Replaces store_kvcache / store_kvcache_kernel
+ * (nanovllm/layers/attention.py:10-40): for every token i with
+ * slot_mapping[i] != -1, row i of key/value (num_kv_heads*head_dim contiguous
+ * elements, rows `key_row_stride` / `value_row_stride` elements apart) is
+ * written to slot slot_mapping[i] of k_cache / v_cache.  With
+ * kv_dtype == SLO_KV_FP8_E4M3FN it implements the store of the quantised pool
+ * specified in docs/project_manual.md:527-537,583: per (token, kv head)
+ *   amax = max|x|; scale = amax == 0 ? 1 : max(amax / 448, scale_floor)
+ *   code = E4M3FN_RNE(clamp(x / scale, -448, 448)); k_scale[slot, head] = scale
+ * key/value are bf16.  Slots outside [0, num_slots) are skipped like -1.
+ */
+int slo_store_kvcache(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      const int32_t* slot_mapping, int32_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t kv_dtype,
+                      void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                      int64_t num_slots, float scale_floor, slo_stream_t stream);
+
+/*
+ * Arguments of one ragged paged-attention launch.  Query rows [0, num_decode)
+ * are decode rows (one query each, attending to decode_lens[b] cached tokens
+ * through decode_tables[b]); query rows num_decode + [cu_q[r], cu_q[r+1]) are
+ * the queries of prefill row r, attending causally (bottom-right aligned:
+ * key j is visible to query i iff j <= i + Lk - Lq) to Lk = cu_k[r+1]-cu_k[r]
+ * keys read from the pool through prefill_tables[r], or, when
+ * prefill_tables is NULL, from the contiguous new K/V rows k/v starting at
+ * row cu_k[r].  GQA maps query head h to kv head h / (num_heads/num_kv_heads).
+ */
+typedef struct slo_paged_attention_args {
+  const void* q;              /* bf16 [num_q_rows, num_heads, head_dim] */
+  int64_t q_row_stride;       /* elements between query rows */
+  void* out;                  /* bf16 [num_q_rows, num_heads, head_dim] */
+  int64_t out_row_stride;
+  int32_t num_q_rows;
+
+  const void* k_cache;        /* pool, see file comment */
+  const void* v_cache;
+  const float* k_scale;       /* FP8 only, else NULL */
+  const float* v_scale;
+  int32_t kv_dtype;
+  int32_t num_blocks;
+  int32_t block_size;         /* multiple of 64 */
+
+  int32_t num_decode;
+  const int32_t* decode_lens;     /* [num_decode] */
+  const int32_t* decode_tables;   /* [num_decode, >= decode_table_width], -1 padded */
+  int32_t decode_table_stride;
+  int32_t decode_table_width;
+
+  int32_t num_prefill;
+  const int32_t* prefill_cu_q;    /* [num_prefill + 1] */
+  const int32_t* prefill_cu_k;    /* [num_prefill + 1] */
+  int32_t max_q;                  /* host bounds: max over rows of Lq and Lk */
+  int32_t max_k;
+  const int32_t* prefill_tables;  /* [num_prefill, >= width] or NULL */
+  int32_t prefill_table_stride;
+  int32_t prefill_table_width;
+  const void* k;                  /* contiguous bf16 K/V, used iff prefill_tables == NULL */
+  int64_t k_row_stride;
+  const void* v;
+  int64_t v_row_stride;
+  int32_t num_kv_rows;
+
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;               /* 128 */
+  float softmax_scale;
+
+  void* workspace;                /* zero-filled once at allocation */
+  size_t workspace_bytes;
+  int32_t phases;                 /* SLO_PHASE_* mask */
+} slo_paged_attention_args;
+
+/*
+ * Bytes of workspace one launch needs when at most `max_decode_rows` decode
+ * rows of at most `max_decode_len` tokens each are present.
+ */
+int slo_attention_workspace_bytes(int32_t max_decode_rows, int32_t max_decode_len,
+                                  int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, size_t* bytes);
+
+/*
+ * One launch of the ragged mixed prefill/decode paged attention.
+ *
+ * Replaces, in one kernel, the per-phase flash-attn calls of forward_mixed
+ * (nanovllm/layers/mixed_attention.py:36-57: flash_attn_with_kvcache on rows
+ * [:d], flash_attn_varlen_func on rows [d:], torch.cat), the V0 decode call
+ * (nanovllm/layers/attention.py:75-78) and the V0 prefill call
+ * (nanovllm/layers/attention.py:68-74).  The work list (split-K decode chunks
+ * and prefill query tiles) is built on the GPU from the metadata, and split-K
+ * partials are merged inside the same launch.  Launches that share one
+ * workspace must be ordered on one stream.
+ */
+int slo_paged_attention(const slo_paged_attention_args* args, slo_stream_t stream);
+
+/* Description of the last error on the calling thread ("" if none). */
+const char* slo_last_error(void);
+
+/* Size of slo_paged_attention_args, for binding checks. */
+size_t slo_paged_attention_args_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLO_ATTN_H_ */

@@ -1,0 +1,18 @@
+"""MI355X (gfx950) attention hot path for the SLO-aware nano-vLLM engine.
+
+Host layer in Python over hand-written HIP kernels behind a C-ABI
+(include/slo_attn.h, built into libslo_attn.so next to this file):
+``store_kvcache`` (slot-mapped KV write, optional E4M3FN quantisation) and one
+ragged mixed prefill/decode paged-attention launch, exposed through the same
+``Attention`` / ``forward_mixed`` / ``Context`` interfaces as the reference.
+"""
+from .context import Context, get_context, reset_context, set_context
+from .mixed_attention import MixedAttentionContext, forward_mixed
+from .ops import paged_attention, reserve_workspace, store_kvcache
+from .attention import Attention
+from . import _lib
+
+__all__ = [
+    "Attention", "Context", "MixedAttentionContext", "forward_mixed", "get_context",
+    "paged_attention", "reserve_workspace", "reset_context", "set_context", "store_kvcache",
+]

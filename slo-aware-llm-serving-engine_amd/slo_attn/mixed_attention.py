@@ -1,0 +1,62 @@
+"""V1 mixed step: one KV write and ONE ragged attention launch.
+
+Mirrors nanovllm/layers/mixed_attention.py:15-57.  ``MixedAttentionContext``
+keeps the reference's fields, order and defaults, so ``prepare_mixed``
+(nanovllm/engine/mixed_model_runner.py:66-92) fills it unchanged.  Where the
+reference issues flash_attn_with_kvcache on the decode rows ``[:d]``, then
+flash_attn_varlen_func on the prefill rows ``[d:]`` and a ``torch.cat``, this
+module issues a single HIP launch that writes both phases into one output.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .ops import paged_attention
+
+
+@dataclass
+class MixedAttentionContext:
+    num_decode: int
+    num_prefill_tokens: int
+    decode_lens: torch.Tensor | None
+    decode_tables: torch.Tensor | None
+    prefill_cu_q: torch.Tensor | None
+    prefill_cu_k: torch.Tensor | None
+    prefill_tables: torch.Tensor | None
+    max_q: int
+    max_k: int
+    prefill_has_history: bool = True
+
+
+def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
+                  k_scale=None, v_scale=None, phases=_lib.PHASE_ALL):
+    """Write all new K/V first, then attend: decode rows first, prefill after.
+
+    Same arguments as the reference (mixed_attention.py:29).  ``k_scale`` /
+    ``v_scale`` are the fp32 scale pools of an E4M3FN cache.  ``phases``
+    restricts the launch to decode or prefill rows (the split mode that mirrors
+    the reference's per-phase calls); rows of the other phase are left
+    untouched in the returned tensor.
+    """
+    meta = context.mixed
+    if not k_cache.numel() or not v_cache.numel():
+        raise RuntimeError("mixed forward requires an allocated KV pool")
+    if k_scale is None:
+        store_fn(k, v, k_cache, v_cache, context.slot_mapping)
+    else:
+        store_fn(k, v, k_cache, v_cache, context.slot_mapping, k_scale, v_scale)
+    d = meta.num_decode
+    num_prefill = 0
+    if meta.num_prefill_tokens:
+        num_prefill = meta.prefill_cu_q.numel() - 1
+    history = bool(meta.prefill_has_history)
+    return paged_attention(
+        q, k_cache, v_cache, scale, num_kv_heads=k.shape[1], k_scale=k_scale, v_scale=v_scale,
+        num_decode=d, decode_lens=meta.decode_lens, decode_tables=meta.decode_tables,
+        num_prefill=num_prefill, prefill_cu_q=meta.prefill_cu_q, prefill_cu_k=meta.prefill_cu_k,
+        max_q=meta.max_q, max_k=meta.max_k,
+        prefill_tables=meta.prefill_tables if history else None,
+        k=None if history else k[d:], v=None if history else v[d:], phases=phases)
