@@ -1,0 +1,259 @@
+"""Benchmark of the per-layer attention step on one MI355X.
+
+Workload: the V1 mixed ragged batch of Qwen3-4B attention (32 query heads,
+8 kv heads, head_dim 128, 256-token pages): 24 decode rows with contexts drawn
+uniform in [256, 4096] (seed 3) plus two 512-token prefill chunks with cached
+prefixes 0 and 1024, 1048 new tokens, 512-page pool.  One step = the
+slot-mapped KV write of the 1048 new tokens + ONE ragged attention launch.
+
+* value: whole-step throughput in tokens/s (1048 tokens per step), from HIP
+  graph replays of 4 consecutive steps that rotate over 4 copies of the pool
+  (4 x 512 MiB) so that no step finds its KV in the 256 MB Infinity Cache.
+* roofline: the fused attention kernel against HBM bandwidth; achieved =
+  algorithmic bytes per launch (decode KV bytes + prefill K/V + q + out) /
+  average launch duration (HIP events around the launch on its stream; a
+  spin kernel queued ahead keeps host launch latency out of the interval, and
+  consecutive launches rotate over the 4 pool copies so the KV is read from
+  HBM, not from the Infinity Cache).  roofline_decode / roofline_prefill
+  time the split launches (decode rows only against HBM, prefill rows only
+  against bf16 MFMA peak), the mode that mirrors the reference's per-phase
+  flash-attn calls.
+* cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
+  step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "slo-aware-llm-serving-engine_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "mixed-step attn tokens/s; decode KV HBM GB/s (% of peak); prefill MFMA util"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16")
+    ap.add_argument("--events", type=int, default=100, help="event-timed launches per mode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the attention path runs at TP=1 and this build has no multi-GPU path).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from slo_attn import _lib, forward_mixed, reserve_workspace, store_kvcache, workloads
+    from slo_attn.ops import paged_attention
+    from types import SimpleNamespace
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    w = workloads.config(3)
+    fp8 = args.kv == "fp8"
+    dev = workloads.to_device(w, device)
+    meta, slots = dev["meta"], dev["slot_mapping"]
+    q, k, v = dev["q"], dev["k"], dev["v"]
+    ctx = SimpleNamespace(mixed=meta, slot_mapping=slots)
+    nsets = 4
+    pools = []
+    base_k, base_v = w.k_cache.to(device), w.v_cache.to(device)
+    for _ in range(nsets):
+        if fp8:
+            nblk, bs, hkv, d = base_k.shape
+            kc = torch.empty(nblk, bs, hkv, d, dtype=torch.uint8, device=device)
+            vc = torch.empty_like(kc)
+            ks = torch.empty(nblk, bs, hkv, dtype=torch.float32, device=device)
+            vs = torch.empty_like(ks)
+            allslots = torch.arange(nblk * bs, dtype=torch.int32, device=device)
+            store_kvcache(base_k.view(-1, hkv, d), base_v.view(-1, hkv, d), kc, vc, allslots, ks, vs)
+            pools.append((kc, vc, ks, vs))
+        else:
+            pools.append((base_k.clone(), base_v.clone(), None, None))
+    del base_k, base_v
+    torch.cuda.synchronize()
+    reserve_workspace(device, w.num_decode, max(len(t) for t in w.decode_tables) * w.block_size, 32, 8, 128)
+
+    def step(i, phases=_lib.PHASE_ALL):
+        kc, vc, ks, vs = pools[i % nsets]
+        return forward_mixed(q, k, v, kc, vc, ctx, w.scale, store_kvcache, ks, vs, phases=phases)
+
+    def attn_only(i, phases):
+        kc, vc, ks, vs = pools[i % nsets]
+        return paged_attention(
+            q, kc, vc, w.scale, num_kv_heads=8, k_scale=ks, v_scale=vs, num_decode=meta.num_decode,
+            decode_lens=meta.decode_lens, decode_tables=meta.decode_tables,
+            num_prefill=meta.prefill_cu_q.numel() - 1, prefill_cu_q=meta.prefill_cu_q,
+            prefill_cu_k=meta.prefill_cu_k, max_q=meta.max_q, max_k=meta.max_k,
+            prefill_tables=meta.prefill_tables, phases=phases, out=out_buf)
+
+    out_buf = torch.empty_like(q)
+    for i in range(max(args.warmup, 4)):
+        step(i)
+    torch.cuda.synchronize()
+
+    # ---- whole-step throughput from graph replays (4 steps per replay)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(nsets):
+            step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for i in range(nsets):
+            step(i)
+    for _ in range(max(1, args.warmup // nsets)):
+        graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, (args.steps + nsets - 1) // nsets)
+    steps = replays * nsets
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / steps
+    tokens = w.num_tokens
+    value = tokens * steps / elapsed
+
+    # ---- per-launch kernel durations (HIP events on the launch stream, cold cache)
+    def launch_times(phases):
+        stream = torch.cuda.current_stream()
+        times = []
+        for i in range(args.events + 3):
+            torch.cuda._sleep(200_000)  # GPU-side backlog: the events bracket only the launch
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            attn_only(i, phases)
+            e1.record(stream)
+            e1.synchronize()
+            if i >= 3:
+                times.append(e0.elapsed_time(e1) * 1e3)  # us
+        return statistics.mean(times), statistics.median(times)
+
+    t_fused, t_fused_med = launch_times(_lib.PHASE_ALL)
+    t_dec, t_dec_med = launch_times(_lib.PHASE_DECODE)
+    t_pre, t_pre_med = launch_times(_lib.PHASE_PREFILL)
+
+    elem = 1.0 if fp8 else 2.0
+    scale_b = 4 if fp8 else 0
+    dec_bytes = w.decode_kv_bytes(elem, scale_b)
+    hq, hkv, d = 32, 8, 128
+    pre_kv_tokens = sum(n + p for n, p in zip(w.prefill_q, w.prefill_prefix))
+    pre_bytes = pre_kv_tokens * hkv * (2 * d * elem + 2 * scale_b)
+    qo_bytes = 2 * tokens * hq * d * 2
+    fused_bytes = dec_bytes + pre_bytes + qo_bytes
+    flops = w.prefill_flops()
+    fused_gbs = fused_bytes / (t_fused * 1e-6) / 1e9
+    dec_gbs = (dec_bytes + 2 * w.num_decode * hq * d * 2) / (t_dec * 1e-6) / 1e9
+    pre_tflops = flops / (t_pre * 1e-6) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, fp8)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), unit-RMS q/k)",
+        "config": {
+            "workload": w.name, "decode_rows": w.num_decode, "decode_context_sum": sum(w.decode_lens),
+            "prefill_chunks": w.prefill_q, "prefill_prefixes": w.prefill_prefix, "new_tokens": tokens,
+            "heads": [hq, hkv, d], "block_size": w.block_size, "kv_cache": args.kv,
+            "step": "store_kvcache + one fused ragged attention launch", "pool_copies_rotated": nsets,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(fused_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "paged_attention_kernel (fused decode+prefill)",
+            "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(t_fused, 2),
+            "median_launch_us": round(t_fused_med, 2),
+        },
+        "roofline_decode": {
+            "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "decode_kv_bytes": dec_bytes,
+            "avg_launch_us": round(t_dec, 2), "median_launch_us": round(t_dec_med, 2),
+        },
+        "roofline_prefill": {
+            "bound": "mfma", "achieved": round(pre_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(pre_tflops / BF16_PEAK_TFLOPS, 4), "flops": flops,
+            "avg_launch_us": round(t_pre, 2), "median_launch_us": round(t_pre_med, 2),
+        },
+        "split_step_us": round(t_dec + t_pre, 2),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(w, fp8):
+    """The CPU oracle (fp32 torch on the host cores) on the same step."""
+    import numpy as np
+    import torch
+    from oracle import attention as oatt
+    from oracle import fp8 as ofp8
+    from oracle import kvstore
+    from slo_attn.workloads import padded_tables
+
+    meta = {
+        "num_decode": w.num_decode, "num_prefill_tokens": sum(w.prefill_q), "decode_lens": w.decode_lens,
+        "decode_tables": padded_tables(w.decode_tables), "prefill_cu_q": w.cu_q, "prefill_cu_k": w.cu_k,
+        "prefill_tables": padded_tables(w.prefill_tables), "prefill_has_history": w.has_history,
+    }
+    kc = w.k_cache.clone()
+    vc = w.v_cache.clone()
+    if fp8:
+        kcodes, kscale = ofp8.quantize_kv(kc.float().numpy())
+        vcodes, vscale = ofp8.quantize_kv(vc.float().numpy())
+
+    def run():
+        if fp8:
+            kvstore.store_kvcache_fp8(w.k.float().numpy(), w.v.float().numpy(), kcodes, vcodes, kscale, vscale,
+                                      w.slot_mapping)
+            kf = torch.from_numpy(ofp8.dequantize_kv(kcodes, kscale))
+            vf = torch.from_numpy(ofp8.dequantize_kv(vcodes, vscale))
+        else:
+            kvstore.store_kvcache(w.k.view(torch.int16).numpy(), w.v.view(torch.int16).numpy(),
+                                  kc.view(torch.int16).numpy(), vc.view(torch.int16).numpy(), w.slot_mapping)
+            kf, vf = kc, vc
+        return oatt.mixed(w.q.float(), w.k.float(), w.v.float(), kf, vf, meta, w.scale)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(w.num_tokens / t, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"full step ({w.num_tokens} tokens), median of 3 after 1 warm-up, "
+                                      f"{t * 1e3:.1f} ms per step"}
+
+
+if __name__ == "__main__":
+    main()

@@ -4,28 +4,41 @@
 // (nanovllm/layers/mixed_attention.py:36-57) and of the V0 branches of
 // Attention.forward (nanovllm/layers/attention.py:68-78).
 //
-// Work list.  Every workgroup (4 wavefronts) first derives, from the metadata
-// alone, the number of work items of every row and their exclusive prefix
-// (prefill rows first, then decode rows), then pulls item indices from a
-// device counter until the list is exhausted.  The grid is sized from
-// capacities, never from device data, so the launch can be recorded in a HIP
-// graph.  The counter and the split-K tickets reset themselves at the end of
-// every launch, so no memset is ever needed.
+// Work list.  Every workgroup (4 wavefronts, two workgroups per CU) first
+// derives, from the metadata alone, the number of work items of every row and
+// their exclusive prefix (prefill rows first, then decode rows), then pulls
+// item indices from a device counter (one fetch ahead) until the list is
+// exhausted.  The grid is sized from capacities, never from device data, so
+// the launch can be recorded in a HIP graph.  The counter and the split-K
+// tickets reset themselves at the end of every launch, so no memset is needed.
 //
-//  * Prefill item (row r, query block of BQ positions, kv head h): each
+//  * Prefill item (row r, block of 32 query positions, kv head h): each
 //    wavefront owns one of the G query heads that share kv head h, for the
-//    same BQ positions, so the K/V tiles staged in LDS serve all G heads.  The
-//    contraction runs on bf16 MFMA (v_mfma_f32_16x16x32_bf16) in the
-//    transposed form S^T = K Q^T, O^T += V^T P^T, which keeps each query
-//    column's softmax statistics lane-local: the S^T accumulator is the B
-//    operand of the PV product without any data movement, and V^T comes from
-//    the natural [token][d] LDS tile through ds_read_b64_tr_b16.
+//    same positions, so the K/V tiles staged in LDS serve all G heads.  Tiles
+//    of 64 keys are double-buffered: the next tile's global loads are in
+//    flight while the current one is consumed.  The contraction runs on bf16
+//    MFMA (v_mfma_f32_16x16x32_bf16) in the transposed form S^T = K Q^T,
+//    O^T += V^T P^T, which keeps each query column's softmax statistics
+//    lane-local: the S^T accumulator is the B operand of the PV product
+//    without data movement, and V^T comes from the natural [token][d] LDS tile
+//    through ds_read_b64_tr_b16.
 //  * Decode item (row b, chunk of 256 tokens, kv head h): each wavefront takes
 //    64 tokens; the G query heads sharing h are the MFMA columns, K goes from
-//    HBM straight into MFMA A-operand registers, V is staged in LDS for the
-//    transposed read.  The 4 wavefronts merge in LDS; when a row has several
-//    chunks, each writes an (m, l, acc) partial and the last chunk to finish
-//    (device-scope ticket) merges them (docs/project_manual.md:643-650).
+//    HBM straight into MFMA A-operand registers, V goes from HBM straight into
+//    LDS (global_load_lds_dwordx4) for the transposed read.  The 4 wavefronts
+//    merge in LDS; a row with several chunks writes one (m, l, acc) partial per
+//    chunk and the last chunk to finish merges them (the split-K merge of
+//    docs/project_manual.md:643-650).
+//
+// LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
+// XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 2*(row & 7)), so the MFMA
+// operand reads of 16 lanes fall on distinct banks.
+//
+// Split-K visibility across XCDs: partials are written and read with
+// agent-scope atomic stores/loads (global_store/load ... sc1), which bypass
+// the per-XCD L2; each writer waits for its stores to be acknowledged
+// (s_waitcnt vmcnt(0)) and the workgroup barrier orders them before the
+// ticket increment.  No L2 writeback or invalidate is needed.
 //
 // Softmax runs in the log2 domain (scores scaled by softmax_scale*log2(e),
 // exp2 on v_exp_f32).  Fully-masked tiles never produce exp(-inf - -inf).
@@ -42,14 +55,19 @@
 
 namespace slo {
 
-constexpr int HD = 128;         // head_dim this kernel implements
-constexpr int NT = 256;         // threads per workgroup (4 wavefronts)
-constexpr int TT = 64;          // tokens per wavefront tile
-constexpr int CHUNK = 4 * TT;   // decode split-K chunk
-constexpr int ROW = HD + 8;     // LDS row pitch in bf16 (272 bytes)
-constexpr int MAX_ROWS = 2048;  // decode + prefill rows per launch
-constexpr int MAX_G = 16;       // query heads per kv head
-constexpr int CTRL_BYTES = 256;
+constexpr int HD = 128;                // head_dim this kernel implements
+constexpr int NT = 256;                // threads per workgroup (4 wavefronts)
+constexpr int TT = 64;                 // tokens per tile
+constexpr int CHUNK = 4 * TT;          // decode split-K chunk
+constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
+constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
+constexpr int NQT = 2;                 // 16-position column tiles per prefill wavefront
+constexpr int BQ = 16 * NQT;           // query positions per prefill item
+constexpr int MAX_ROWS = 1024;         // decode + prefill rows per launch
+constexpr int MAX_G = 16;              // query heads per kv head
+constexpr int NLIST = 8;          // work lists (one per XCD)
+constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
+constexpr int CTRL_BYTES = NLIST * CTRL_STRIDE * 4;
 constexpr int MAX_COUNTERS = 65536;
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -66,7 +84,7 @@ struct Params {
   const float* v_scale;
   int32_t num_blocks;
   int32_t block_size;
-  int32_t nd;  // decode rows taking part in this launch
+  int32_t nd;             // decode rows taking part in this launch
   int32_t q_off_prefill;  // first query row of prefill row 0
   const int32_t* dlens;
   const int32_t* dtab;
@@ -87,37 +105,42 @@ struct Params {
   int32_t G;
   int32_t HG;  // ceil(G / 4): wavefront groups per kv head in prefill
   float scale_log2;
-  int* ctrl;      // [0] next item, [1] finished workgroups
+  int* ctrl;      // per list: [0] fetch counter, [1] base of the current launch
   int* counters;  // split-K tickets, [num_decode * hkv]
   float* partials;
 };
 
-template <int NQT>
 struct Smem {
   union {
-    uint16_t dec_v[4][TT * ROW];  // decode: one V tile per wavefront
+    uint8_t dec_v[4][TILE_BYTES];  // decode: one V tile per wavefront
     struct {
-      uint16_t k[TT * ROW];
-      uint16_t v[TT * ROW];
-      float ks[TT];
-      float vs[TT];
-    } pf;
-    struct {
-      float o[4][MAX_G][HD];
-      float m[4][MAX_G];
-      float l[4][MAX_G];
-    } mg;
+      uint8_t k[2][TILE_BYTES];
+      uint8_t v[2][TILE_BYTES];
+    } pf;                          // prefill: double-buffered K/V tiles
   } u;
+  struct {
+    float o[4][4][HD];
+    float m[4][4];
+    float l[4][4];
+  } mg;                            // decode: cross-wavefront merge, 4 query heads per pass
+  float ks[2][TT];
+  float vs[2][TT];
   int off[MAX_ROWS + 1];
   int wsum[4];
-  int item;
+  uint32_t item;
+  uint32_t base;
   int row;
   int last;
+  int salt;
 };
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Byte offset of 16-byte chunk `c` of tile row `r` (K and V swizzles).
+__device__ __forceinline__ int k_off(int r, int c) { return r * ROWB + ((c ^ (r & 15)) << 4); }
+__device__ __forceinline__ int v_off(int r, int c) { return r * ROWB + ((c ^ ((r & 7) << 1)) << 4); }
 
 __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(const u32x2& w) {
   const u32x2 a = fp8x4_to_bf16x4(w.x), b = fp8x4_to_bf16x4(w.y);
@@ -129,9 +152,9 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(const u32x2& w) {
   return r;
 }
 
-__device__ __forceinline__ s16x4 lds_tr16(const uint16_t* p) {
+__device__ __forceinline__ s16x4 lds_tr16(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(const_cast<uint16_t*>(p)));
+      (__attribute__((address_space(3))) s16x4*)(const_cast<uint8_t*>(p)));
 }
 
 __device__ __forceinline__ bf16x8 join_tr(const s16x4& a, const s16x4& b) {
@@ -143,14 +166,22 @@ __device__ __forceinline__ bf16x8 join_tr(const s16x4& a, const s16x4& b) {
   return as_bf16x8(r);
 }
 
+// V^T as the A operand of O^T = V^T P^T for k-step `ks` (32 tokens) and
+// d-tile `dt`: lane (n, g) receives d = 16dt + n of tokens 32ks + 4g + {0..3}
+// (slots 0-3) and 32ks + 16 + 4g + {0..3} (slots 4-7).
+__device__ __forceinline__ bf16x8 vt_operand(const uint8_t* tile, int ks, int dt, int g, int n) {
+  const int r0 = 32 * ks + 4 * g + (n >> 2);
+  const int c = 2 * dt + ((n & 3) >> 1);
+  const int half = (n & 1) << 3;
+  return join_tr(lds_tr16(tile + v_off(r0, c) + half), lds_tr16(tile + v_off(r0 + 16, c) + half));
+}
+
 __device__ __forceinline__ int decode_len(const Params& p, int b) {
   const int L = p.dlens[b];
   return min(max(L, 0), p.dtab_width * p.block_size);
 }
 
-template <int NQT>
 __device__ __forceinline__ int row_items(const Params& p, int r) {
-  constexpr int BQ = 16 * NQT;
   if (r < p.np) {
     const int lq = p.cu_q[r + 1] - p.cu_q[r];
     return lq > 0 ? ((lq + BQ - 1) / BQ) * p.hkv * p.HG : 0;
@@ -159,16 +190,41 @@ __device__ __forceinline__ int row_items(const Params& p, int r) {
   return max(1, (L + CHUNK - 1) / CHUNK) * p.hkv;
 }
 
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------- decode item
-template <bool FP8, int NQT>
-__device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, int dindex) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// A decode item is split in three steps so that the next item's HBM loads can
+// be in flight while the current item finishes: issue (metadata, Q/K loads to
+// registers, V HBM -> LDS), compute (QK, softmax, PV into registers) and tail
+// (cross-wavefront merge, split-K partial / ticket / final merge, output).
+struct DecodeState {
+  int b, h, c, nch, ntok, dindex;
+  int64_t slot0;
+  u32x4 qv[4];
+  u32x4 k[4][4];   // bf16 K operand (bf16 pool)
+  u32x2 k8[4][4];  // raw E4M3FN K bytes (E4M3FN pool)
+  u32x2 vraw[16];  // raw E4M3FN V rows (bf16 V goes straight to LDS)
+  float ksc, vsc;  // E4M3FN scales of token `lane` of this wavefront's tile
+};
+
+template <bool FP8>
+__device__ __forceinline__ void decode_issue(const Params& p, Smem& sm, DecodeState& st, int b, int local,
+                                             int dindex, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int G = p.G;
-  const int h = local % p.hkv, c = local / p.hkv;
+  st.b = b;
+  st.h = local % p.hkv;
+  st.c = local / p.hkv;
+  st.dindex = dindex;
   const int L = decode_len(p, b);
-  const int nch = max(1, (L + CHUNK - 1) / CHUNK);
-  const int t0 = c * CHUNK + wave * TT;
+  st.nch = max(1, (L + CHUNK - 1) / CHUNK);
+  const int t0 = st.c * CHUNK + wave * TT;
   int ntok = min(max(L - t0, 0), TT);
   int64_t slot0 = 0;
   if (ntok > 0) {
@@ -176,71 +232,81 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
     if (page < 0 || page >= p.num_blocks) ntok = 0;  // never dereference padding
     else slot0 = (int64_t)page * p.block_size + (t0 % p.block_size);
   }
+  st.ntok = ntok;
+  st.slot0 = slot0;
   const int64_t tok_stride = (int64_t)p.hkv * HD;
-  const int64_t head_off = (int64_t)h * HD;
+  const int64_t head_off = (int64_t)st.h * HD;
+  uint8_t* vt = sm.u.dec_v[wave];
 
-  // Q as the B operand: column n is query head h*G+n, k slot (g, st, j) is d = 32g+8st+j.
-  u32x4 qv[4];
-  if (n < G) {
-    const uint16_t* qr = p.q + (int64_t)b * p.q_stride + (int64_t)(h * G + n) * HD + 32 * g;
+  // V tile: row r holds token t0 + r; rows past ntok are zeroed.
+  if constexpr (!FP8) {
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + slot0 * tok_stride + head_off;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qv[st] = ld16(qr + 8 * st);
+    for (int i = 0; i < 16; ++i) {
+      const int r = 4 * i + g;  // == lane / 16 within this 4-row stripe
+      const int chunk = n ^ ((r & 7) << 1);
+      if (r < ntok) __builtin_amdgcn_global_load_lds(vbase + r * tok_stride + 8 * chunk, vt + i * 1024, 16, 0, 0);
+      else st16(vt + r * ROWB + (n << 4), u32x4{0, 0, 0, 0});
+    }
+  } else {
+    const uint8_t* vbase = static_cast<const uint8_t*>(p.v_cache) + slot0 * tok_stride + head_off;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 4 * i + g;
+      const int chunk = n ^ ((r & 7) << 1);
+      st.vraw[i] = r < ntok ? ld8(vbase + r * tok_stride + 8 * chunk) : u32x2{0, 0};
+    }
+  }
+
+  // Q as the B operand: column n is query head h*G+n; k slot (g, st, j) is d = 8(4st+g)+j.
+  if (n < G) {
+    const uint16_t* qr = p.q + (int64_t)b * p.q_stride + (int64_t)(st.h * G + n) * HD;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) st.qv[s4] = ld16(qr + 8 * (4 * s4 + g));
   } else {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qv[st] = u32x4{0, 0, 0, 0};
+    for (int s4 = 0; s4 < 4; ++s4) st.qv[s4] = u32x4{0, 0, 0, 0};
   }
 
   // K as the A operand: row (token) 16mt+n, same k slots.
-  u32x4 ka[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const int tok = 16 * mt + n;
-    if (tok < ntok) {
-      const int64_t e = (slot0 + tok) * tok_stride + head_off + 32 * g;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int64_t e = (slot0 + tok) * tok_stride + head_off + 8 * (4 * s4 + g);
       if constexpr (FP8) {
-        const uint8_t* kr = static_cast<const uint8_t*>(p.k_cache) + e;
-        const u32x4 w0 = ld16(kr), w1 = ld16(kr + 16);
-        ka[mt][0] = fp8x8_to_bf16x8(u32x2{w0.x, w0.y});
-        ka[mt][1] = fp8x8_to_bf16x8(u32x2{w0.z, w0.w});
-        ka[mt][2] = fp8x8_to_bf16x8(u32x2{w1.x, w1.y});
-        ka[mt][3] = fp8x8_to_bf16x8(u32x2{w1.z, w1.w});
+        st.k8[mt][s4] = tok < ntok ? ld8(static_cast<const uint8_t*>(p.k_cache) + e) : u32x2{0, 0};
       } else {
-        const uint16_t* kr = static_cast<const uint16_t*>(p.k_cache) + e;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) ka[mt][st] = ld16(kr + 8 * st);
+        st.k[mt][s4] = tok < ntok ? ld16(static_cast<const uint16_t*>(p.k_cache) + e) : u32x4{0, 0, 0, 0};
       }
-    } else {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) ka[mt][st] = u32x4{0, 0, 0, 0};
     }
   }
 
-  // V tile -> registers (natural layout): lane covers token 4*it+g, chunk n.
-  u32x4 vr[16];
-#pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int tok = 4 * it + g;
-    if (tok < ntok) {
-      const int64_t e = (slot0 + tok) * tok_stride + head_off + 8 * n;
-      if constexpr (FP8) vr[it] = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + e));
-      else vr[it] = ld16(static_cast<const uint16_t*>(p.v_cache) + e);
-    } else {
-      vr[it] = u32x4{0, 0, 0, 0};
-    }
-  }
-
-  float ksc[4][4], vsc[4][4];
   if constexpr (FP8) {
+    const bool ok = lane < ntok;
+    const int64_t si = (slot0 + lane) * p.hkv + st.h;
+    st.ksc = ok ? p.k_scale[si] : 0.0f;
+    st.vsc = ok ? p.v_scale[si] : 0.0f;
+  }
+}
+
+// QK, softmax and PV of the issued item.  Leaves this wavefront's O^T
+// accumulators (lane (n, g): head n, d = 16dt + 4g + i), its max and its sum.
+template <bool FP8>
+__device__ __forceinline__ void decode_compute(const Params& p, Smem& sm, DecodeState& st, int tid, f32x4 (&o)[8],
+                                               float& mx_out, float& ls_out) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int ntok = st.ntok;
+  uint8_t* vt = sm.u.dec_v[wave];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st16(vt + (4 * i + g) * ROWB + (n << 4), fp8x8_to_bf16x8(st.vraw[i]));
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * mt + 4 * g + i;
-        const bool ok = tok < ntok;
-        const int64_t si = (slot0 + tok) * p.hkv + h;
-        ksc[mt][i] = ok ? p.k_scale[si] : 0.0f;
-        vsc[mt][i] = ok ? p.v_scale[si] : 0.0f;
-      }
+      for (int s4 = 0; s4 < 4; ++s4) st.k[mt][s4] = fp8x8_to_bf16x8(st.k8[mt][s4]);
   }
 
   // S^T = K Q^T for the wavefront's 64 tokens.
@@ -249,7 +315,7 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
   for (int mt = 0; mt < 4; ++mt) {
     s[mt] = f32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) s[mt] = mfma16(as_bf16x8(ka[mt][st]), as_bf16x8(qv[st]), s[mt]);
+    for (int s4 = 0; s4 < 4; ++s4) s[mt] = mfma16(as_bf16x8(st.k[mt][s4]), as_bf16x8(st.qv[s4]), s[mt]);
   }
 
   float mx = NEG_INF;
@@ -259,7 +325,7 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
     for (int i = 0; i < 4; ++i) {
       const int tok = 16 * mt + 4 * g + i;
       float x = s[mt][i] * p.scale_log2;
-      if constexpr (FP8) x *= ksc[mt][i];
+      if constexpr (FP8) x *= __shfl(st.ksc, tok, 64);
       x = tok < ntok ? x : NEG_INF;
       s[mt][i] = x;
       mx = fmaxf(mx, x);
@@ -274,7 +340,8 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
     for (int i = 0; i < 4; ++i) {
       const float e = __builtin_amdgcn_exp2f(s[mt][i] - mu);
       ls += e;
-      s[mt][i] = FP8 ? e * vsc[mt][i] : e;
+      if constexpr (FP8) s[mt][i] = e * __shfl(st.vsc, 16 * mt + 4 * g + i, 64);
+      else s[mt][i] = e;
     }
   ls += __shfl_xor(ls, 16, 64);
   ls += __shfl_xor(ls, 32, 64);
@@ -291,66 +358,70 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
     pb[ks] = as_bf16x8(w);
   }
 
-  uint16_t* vl = sm.u.dec_v[wave];
-#pragma unroll
-  for (int it = 0; it < 16; ++it) st16(vl + (4 * it + g) * ROW + 8 * n, vr[it]);
+  // The V tile (LDS DMA, zero rows or decoded E4M3FN rows) must have landed.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-
-  f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
-  const int src_tok = n >> 2, src_col = 4 * (n & 3);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* a0 = vl + (32 * ks + 4 * g + src_tok) * ROW + 16 * dt + src_col;
-      const bf16x8 vt = join_tr(lds_tr16(a0), lds_tr16(a0 + 16 * ROW));
-      o[dt] = mfma16(vt, pb[ks], o[dt]);
-    }
-  __syncthreads();  // the merge area aliases the V tiles
+    for (int dt = 0; dt < 8; ++dt) o[dt] = mfma16(vt_operand(vt, ks, dt, g, n), pb[ks], o[dt]);
+  mx_out = mx;
+  ls_out = ls;
+}
 
-  if (n < G) {
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.u.mg.o[wave][n][16 * dt + 4 * g + i] = o[dt][i];
-    if (g == 0) {
-      sm.u.mg.m[wave][n] = mx;
-      sm.u.mg.l[wave][n] = ls;
-    }
-  }
-  __syncthreads();
-
+// Cross-wavefront merge through LDS, then either the output (single chunk) or
+// the split-K partial + ticket, and the final merge by the last chunk.
+__device__ __forceinline__ void decode_tail(const Params& p, Smem& sm, int b, int h, int c, int nch, int dindex,
+                                            int tid, const f32x4 (&o)[8], float mx, float ls) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int G = p.G;
   float* part = p.partials + (size_t)dindex * G * (HD + 2);
-  for (int idx = tid; idx < G * HD; idx += NT) {
-    const int hn = idx / HD, d = idx % HD;
-    float M = NEG_INF;
+  for (int hg = 0; hg < G; hg += 4) {  // 4 query heads per pass through the merge area
+    __syncthreads();
+    if (n >= hg && n < min(G, hg + 4)) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.u.mg.m[w][hn]);
-    float Ls = 0.0f, O = 0.0f;
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = sm.u.mg.m[w][hn];
-      const float f = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      Ls += f * sm.u.mg.l[w][hn];
-      O += f * sm.u.mg.o[w][hn][d];
+        for (int i = 0; i < 4; ++i) sm.mg.o[wave][n - hg][16 * dt + 4 * g + i] = o[dt][i];
+      if (g == 0) {
+        sm.mg.m[wave][n - hg] = mx;
+        sm.mg.l[wave][n - hg] = ls;
+      }
     }
-    if (nch == 1) {
-      p.out[(int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d] =
-          (uint16_t)f32_to_bf16_bits(Ls > 0.0f ? O / Ls : 0.0f);
-    } else {
-      part[hn * HD + d] = O;
-      if (d == 0) {
-        part[G * HD + 2 * hn] = M;
-        part[G * HD + 2 * hn + 1] = Ls;
+    __syncthreads();
+    const int nh = min(4, G - hg);
+    for (int idx = tid; idx < nh * HD; idx += NT) {
+      const int hl = idx / HD, d = idx % HD, hn = hg + hl;
+      float M = NEG_INF;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.mg.m[w][hl]);
+      float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float mw = sm.mg.m[w][hl];
+        const float f = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+        Ls += f * sm.mg.l[w][hl];
+        O += f * sm.mg.o[w][hl][d];
+      }
+      if (nch == 1) {
+        p.out[(int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d] =
+            (uint16_t)f32_to_bf16_bits(Ls > 0.0f ? O / Ls : 0.0f);
+      } else {
+        store_partial(part + hn * HD + d, O);
+        if (d == 0) {
+          store_partial(part + G * HD + 2 * hn, M);
+          store_partial(part + G * HD + 2 * hn + 1, Ls);
+        }
       }
     }
   }
   if (nch == 1) return;
 
   // Split-K: the last chunk of (row, kv head) to finish merges all partials.
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged at the coherence point
   __syncthreads();
   if (tid == 0) {
     const int ticket = atomicAdd(&p.counters[b * p.hkv + h], 1);
@@ -358,22 +429,32 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
   }
   __syncthreads();
   if (!sm.last) return;
-  __threadfence();
   const int first = dindex - (c * p.hkv + h);
+  const size_t pstride = (size_t)p.hkv * G * (HD + 2);  // floats between chunks of one (row, head)
+  const float* p0 = p.partials + (size_t)(first + h) * G * (HD + 2);
   for (int idx = tid; idx < G * HD; idx += NT) {
     const int hn = idx / HD, d = idx % HD;
-    float M = NEG_INF;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float* pc = p.partials + (size_t)(first + cc * p.hkv + h) * G * (HD + 2);
-      M = fmaxf(M, __builtin_nontemporal_load(pc + G * HD + 2 * hn));
-    }
-    float Ls = 0.0f, O = 0.0f;
-    for (int cc = 0; cc < nch; ++cc) {
-      const float* pc = p.partials + (size_t)(first + cc * p.hkv + h) * G * (HD + 2);
-      const float mc = __builtin_nontemporal_load(pc + G * HD + 2 * hn);
-      const float f = mc == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mc - M);
-      Ls += f * __builtin_nontemporal_load(pc + G * HD + 2 * hn + 1);
-      O += f * __builtin_nontemporal_load(pc + hn * HD + d);
+    // One online pass over the chunks; 8 chunks' loads are in flight at a time.
+    float M = NEG_INF, Ls = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 8) {
+      float mc[8], lc[8], oc[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const bool ok = c0 + u < nch;
+        const float* pc = p0 + (size_t)(ok ? c0 + u : c0) * pstride;
+        mc[u] = ok ? load_partial(pc + G * HD + 2 * hn) : NEG_INF;
+        lc[u] = ok ? load_partial(pc + G * HD + 2 * hn + 1) : 0.0f;
+        oc[u] = ok ? load_partial(pc + hn * HD + d) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float mn = fmaxf(M, mc[u]);
+        if (mn == NEG_INF) continue;
+        const float a = __builtin_amdgcn_exp2f(M - mn), bw = __builtin_amdgcn_exp2f(mc[u] - mn);
+        Ls = Ls * a + lc[u] * bw;
+        O = O * a + oc[u] * bw;
+        M = mn;
+      }
     }
     p.out[(int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d] =
         (uint16_t)f32_to_bf16_bits(Ls > 0.0f ? O / Ls : 0.0f);
@@ -382,10 +463,9 @@ __device__ void decode_item(const Params& p, Smem<NQT>& sm, int b, int local, in
 }
 
 // --------------------------------------------------------------- prefill item
-template <bool FP8, int NQT>
-__device__ void prefill_item(const Params& p, Smem<NQT>& sm, int r, int local) {
-  constexpr int BQ = 16 * NQT;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <bool FP8>
+__device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int hg = local % p.HG;
   const int t = local / p.HG;
@@ -411,19 +491,16 @@ __device__ void prefill_item(const Params& p, Smem<NQT>& sm, int r, int local) {
   const bool active = hl < p.G;
   const int hq = h * p.G + hl;
   const int64_t qrow0 = (int64_t)p.q_off_prefill + q_start;
+  const bool src_fp8 = FP8 && paged;
 
   u32x4 qv[NQT][4];
 #pragma unroll
   for (int nt = 0; nt < NQT; ++nt) {
     const int pos = q0 + 16 * nt + n;
-    if (active && pos < Lq && qrow0 + pos < p.num_q_rows) {
-      const uint16_t* qr = p.q + (qrow0 + pos) * p.q_stride + (int64_t)hq * HD + 32 * g;
+    const bool ok = active && pos < Lq && qrow0 + pos < p.num_q_rows;
+    const uint16_t* qr = p.q + (qrow0 + pos) * p.q_stride + (int64_t)hq * HD;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) qv[nt][st] = ld16(qr + 8 * st);
-    } else {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) qv[nt][st] = u32x4{0, 0, 0, 0};
-    }
+    for (int st = 0; st < 4; ++st) qv[nt][st] = ok ? ld16(qr + 8 * (4 * st + g)) : u32x4{0, 0, 0, 0};
   }
 
   f32x4 o[8][NQT];
@@ -436,139 +513,169 @@ __device__ void prefill_item(const Params& p, Smem<NQT>& sm, int r, int local) {
     for (int dt = 0; dt < 8; ++dt) o[dt][nt] = f32x4{0, 0, 0, 0};
   }
 
-  const bool src_fp8 = FP8 && paged;
-  const int src_tok = n >> 2, src_col = 4 * (n & 3);
-  for (int kv0 = 0; kv0 < kend; kv0 += TT) {
+  // Double-buffered tiles: thread covers tile row (tid>>4)+16*it and LDS slot
+  // tid&15 of that row (16-byte chunks XOR-swizzled at load time).  bf16
+  // sources go HBM -> LDS directly (global_load_lds_dwordx4: lane i of a
+  // wavefront lands at byte 16*i of a 1 KiB stripe of 4 rows), so the next
+  // tile is in flight while the current one is consumed; E4M3FN pool bytes are
+  // loaded into registers, decoded, and written to LDS after the current tile's
+  // compute.  Rows past the valid keys are zero.
+  u32x4 kr[4], vr[4];
+  float ksr = 0.0f, vsr = 0.0f;
+  auto issue_tile = [&](int kv0, int buf) {
     const int ntok = min(TT, kend - kv0);
     bool ok = true;
-    int64_t slot0 = 0, base, tstride;
+    int64_t slot0 = 0;
     if (paged) {
       const int page = p.ptab[(int64_t)r * p.ptab_stride + kv0 / p.block_size];
       ok = page >= 0 && page < p.num_blocks;
       slot0 = ok ? (int64_t)page * p.block_size + kv0 % p.block_size : 0;
-      tstride = (int64_t)p.hkv * HD;
-      base = slot0 * tstride + (int64_t)h * HD;
-    } else {
-      tstride = p.k_stride;
-      base = (int64_t)(k_start + kv0) * p.k_stride + (int64_t)h * HD;
     }
-    u32x4 kr[4], vr[4];
+    const int nv = ok ? ntok : 0;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int tok = (tid >> 4) + 16 * it, ch = tid & 15;
-      if (ok && tok < ntok) {
-        if (src_fp8) {
-          const int64_t e = base + tok * tstride + 8 * ch;
-          kr[it] = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.k_cache) + e));
-          vr[it] = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + e));
-        } else if (paged) {
-          const int64_t e = base + tok * tstride + 8 * ch;
-          kr[it] = ld16(static_cast<const uint16_t*>(p.k_cache) + e);
-          vr[it] = ld16(static_cast<const uint16_t*>(p.v_cache) + e);
-        } else {
-          const int64_t ek = (int64_t)(k_start + kv0 + tok) * p.k_stride + (int64_t)h * HD + 8 * ch;
-          const int64_t ev = (int64_t)(k_start + kv0 + tok) * p.v_stride + (int64_t)h * HD + 8 * ch;
-          kr[it] = ld16(p.k + ek);
-          vr[it] = ld16(p.v + ev);
+      const int row = (tid >> 4) + 16 * it;
+      const int kc = (tid & 15) ^ (row & 15);
+      const int vc = (tid & 15) ^ ((row & 7) << 1);
+      if (src_fp8) {
+        u32x4 kx = u32x4{0, 0, 0, 0}, vx = u32x4{0, 0, 0, 0};
+        if (row < nv) {
+          const int64_t e = (slot0 + row) * (int64_t)p.hkv * HD + (int64_t)h * HD;
+          kx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.k_cache) + e + 8 * kc));
+          vx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + e + 8 * vc));
         }
+        kr[it] = kx;
+        vr[it] = vx;
+      } else if (row < nv) {
+        const uint16_t* ks;
+        const uint16_t* vs;
+        if (paged) {
+          const int64_t e = (slot0 + row) * (int64_t)p.hkv * HD + (int64_t)h * HD;
+          ks = static_cast<const uint16_t*>(p.k_cache) + e;
+          vs = static_cast<const uint16_t*>(p.v_cache) + e;
+        } else {
+          const int64_t tk = (int64_t)(k_start + kv0 + row);
+          ks = p.k + tk * p.k_stride + (int64_t)h * HD;
+          vs = p.v + tk * p.v_stride + (int64_t)h * HD;
+        }
+        __builtin_amdgcn_global_load_lds(ks + 8 * kc, sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vs + 8 * vc, sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
       } else {
-        kr[it] = u32x4{0, 0, 0, 0};
-        vr[it] = u32x4{0, 0, 0, 0};
+        st16(sm.u.pf.k[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
+        st16(sm.u.pf.v[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
       }
     }
-    float ksv = 1.0f, vsv = 1.0f;
     if (src_fp8 && tid < TT) {
-      const bool okt = ok && tid < ntok;
+      const bool okt = tid < nv;
       const int64_t si = (slot0 + tid) * p.hkv + h;
-      ksv = okt ? p.k_scale[si] : 0.0f;
-      vsv = okt ? p.v_scale[si] : 0.0f;
+      ksr = okt ? p.k_scale[si] : 0.0f;
+      vsr = okt ? p.v_scale[si] : 0.0f;
     }
-    __syncthreads();  // previous tile fully consumed
+  };
+  auto commit_tile = [&](int buf) {  // register-staged (E4M3FN) tiles only
+    if (!src_fp8) return;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int tok = (tid >> 4) + 16 * it, ch = tid & 15;
-      st16(sm.u.pf.k + tok * ROW + 8 * ch, kr[it]);
-      st16(sm.u.pf.v + tok * ROW + 8 * ch, vr[it]);
+      const int row = (tid >> 4) + 16 * it;
+      st16(sm.u.pf.k[buf] + row * ROWB + ((tid & 15) << 4), kr[it]);
+      st16(sm.u.pf.v[buf] + row * ROWB + ((tid & 15) << 4), vr[it]);
     }
     if (tid < TT) {
-      sm.u.pf.ks[tid] = ksv;
-      sm.u.pf.vs[tid] = vsv;
+      sm.ks[buf][tid] = ksr;
+      sm.vs[buf][tid] = vsr;
     }
-    __syncthreads();
-    if (!active) continue;
+  };
 
-    f32x4 s[4][NQT];
+  if (kend > 0) {
+    issue_tile(0, 0);
+    commit_tile(0);
+  }
+  for (int kv0 = 0, j = 0; kv0 < kend; kv0 += TT, ++j) {
+    const int buf = j & 1;
+    const int ntok = min(TT, kend - kv0);
+    __builtin_amdgcn_s_waitcnt(0);  // this tile's loads have landed in LDS
+    __syncthreads();                // ... for every wavefront; the other buffer is free
+    const bool more = kv0 + TT < kend;
+    if (more) issue_tile(kv0 + TT, buf ^ 1);
+    if (active) {
+      const uint8_t* kt = sm.u.pf.k[buf];
+      const uint8_t* vt = sm.u.pf.v[buf];
+
+      f32x4 s[4][NQT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      u32x4 kf[4];
+      for (int mt = 0; mt < 4; ++mt) {
+        u32x4 kf[4];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) kf[st] = ld16(sm.u.pf.k + (16 * mt + n) * ROW + 32 * g + 8 * st);
+        for (int st = 0; st < 4; ++st) kf[st] = ld16(kt + k_off(16 * mt + n, 4 * st + g));
+#pragma unroll
+        for (int nt = 0; nt < NQT; ++nt) {
+          f32x4 acc = f32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int st = 0; st < 4; ++st) acc = mfma16(as_bf16x8(kf[st]), as_bf16x8(qv[nt][st]), acc);
+          s[mt][nt] = acc;
+        }
+      }
+
+      // Keys that can be masked: beyond the tile's valid rows, or causally
+      // after the earliest query column of the block.
+      const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
+      bf16x8 pb[NQT][2];
 #pragma unroll
       for (int nt = 0; nt < NQT; ++nt) {
-        f32x4 acc = f32x4{0, 0, 0, 0};
+        const int lim = q0 + 16 * nt + n + prefix;  // last visible key index of this column
+        float mx = NEG_INF;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) acc = mfma16(as_bf16x8(kf[st]), as_bf16x8(qv[nt][st]), acc);
-        s[mt][nt] = acc;
-      }
-    }
-
-    bf16x8 pb[NQT][2];
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NQT; ++nt) {
-      const int pos = q0 + 16 * nt + n;
-      const int lim = pos + prefix;  // last visible key index
-      float mx = NEG_INF;
+          for (int i = 0; i < 4; ++i) {
+            const int tok = 16 * mt + 4 * g + i;
+            float x = s[mt][nt][i] * p.scale_log2;
+            if (src_fp8) x *= sm.ks[buf][tok];
+            if (need_mask) x = (tok < ntok && kv0 + tok <= lim) ? x : NEG_INF;
+            s[mt][nt][i] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = wave_max_xor(mx, 16);
+        mx = wave_max_xor(mx, 32);
+        const float mnew = fmaxf(m[nt], mx);
+        const float mu = mnew == NEG_INF ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m[nt] - mu);
+        float rs = 0.0f;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tok = 16 * mt + 4 * g + i;
-          float x = s[mt][nt][i] * p.scale_log2;
-          if (src_fp8) x *= sm.u.pf.ks[tok];
-          x = (tok < ntok && kv0 + tok <= lim) ? x : NEG_INF;
-          s[mt][nt][i] = x;
-          mx = fmaxf(mx, x);
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_amdgcn_exp2f(s[mt][nt][i] - mu);
+            rs += e;
+            s[mt][nt][i] = src_fp8 ? e * sm.vs[buf][16 * mt + 4 * g + i] : e;
+          }
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        l[nt] = l[nt] * alpha + rs;
+        m[nt] = mnew;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          u32x4 w;
+          w.x = pack_bf16x2(s[2 * ks][nt][0], s[2 * ks][nt][1]);
+          w.y = pack_bf16x2(s[2 * ks][nt][2], s[2 * ks][nt][3]);
+          w.z = pack_bf16x2(s[2 * ks + 1][nt][0], s[2 * ks + 1][nt][1]);
+          w.w = pack_bf16x2(s[2 * ks + 1][nt][2], s[2 * ks + 1][nt][3]);
+          pb[nt][ks] = as_bf16x8(w);
         }
-      mx = wave_max_xor(mx, 16);
-      mx = wave_max_xor(mx, 32);
-      const float mnew = fmaxf(m[nt], mx);
-      const float mu = mnew == NEG_INF ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m[nt] - mu);
-      float rs = 0.0f;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(s[mt][nt][i] - mu);
-          rs += e;
-          s[mt][nt][i] = src_fp8 ? e * sm.u.pf.vs[16 * mt + 4 * g + i] : e;
-        }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l[nt] = l[nt] * alpha + rs;
-      m[nt] = mnew;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        u32x4 w;
-        w.x = pack_bf16x2(s[2 * ks][nt][0], s[2 * ks][nt][1]);
-        w.y = pack_bf16x2(s[2 * ks][nt][2], s[2 * ks][nt][3]);
-        w.z = pack_bf16x2(s[2 * ks + 1][nt][0], s[2 * ks + 1][nt][1]);
-        w.w = pack_bf16x2(s[2 * ks + 1][nt][2], s[2 * ks + 1][nt][3]);
-        pb[nt][ks] = as_bf16x8(w);
       }
-    }
 
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* a0 = sm.u.pf.v + (32 * ks + 4 * g + src_tok) * ROW + 16 * dt + src_col;
-        const bf16x8 vt = join_tr(lds_tr16(a0), lds_tr16(a0 + 16 * ROW));
+        for (int dt = 0; dt < 8; ++dt) {
+          const bf16x8 va = vt_operand(vt, ks, dt, g, n);
 #pragma unroll
-        for (int nt = 0; nt < NQT; ++nt) o[dt][nt] = mfma16(vt, pb[nt][ks], o[dt][nt]);
-      }
+          for (int nt = 0; nt < NQT; ++nt) o[dt][nt] = mfma16(va, pb[nt][ks], o[dt][nt]);
+        }
+    }
+    if (more) commit_tile(buf ^ 1);
   }
 
   if (!active) return;
@@ -589,9 +696,9 @@ __device__ void prefill_item(const Params& p, Smem<NQT>& sm, int r, int local) {
 }
 
 // ------------------------------------------------------------------- kernel
-template <bool FP8, int NQT>
-__global__ void __launch_bounds__(NT, 1) paged_attention_kernel(Params p) {
-  __shared__ Smem<NQT> sm;
+template <bool FP8>
+__global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
+  __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
@@ -599,7 +706,7 @@ __global__ void __launch_bounds__(NT, 1) paged_attention_kernel(Params p) {
   const int per = (nrows + NT - 1) / NT;
   const int r0 = tid * per;
   int local_sum = 0;
-  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items<NQT>(p, r);
+  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r);
   int incl = local_sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -612,38 +719,97 @@ __global__ void __launch_bounds__(NT, 1) paged_attention_kernel(Params p) {
   for (int w = 0; w < wave; ++w) run += sm.wsum[w];
   for (int r = r0; r < min(r0 + per, nrows); ++r) {
     sm.off[r] = run;
-    run += row_items<NQT>(p, r);
+    run += row_items(p, r);
   }
   if (tid == NT - 1) sm.off[nrows] = run;
   __syncthreads();
   const int total = sm.off[nrows];
   const int decode_base = sm.off[p.np];
 
-  for (;;) {
-    if (tid == 0) sm.item = atomicAdd(&p.ctrl[0], 1);
+  // Work lists: item i belongs to list i % nlist and workgroup b serves list
+  // b % nlist, so the lists' fetch counters are separate addresses (and, with
+  // round-robin dispatch and 8 kv heads, one kv head's prefill tiles stay on
+  // one XCD's L2).  A list's counter only grows; the list's base is the
+  // counter value at which this launch's items start.  Every workgroup reads
+  // the base before its first fetch and stops after its first fetch past the
+  // list, so a launch makes exactly count + workgroups fetches on a list and
+  // the workgroup that makes the last one advances the base for the next
+  // launch.  No counter is ever reset or contended by a completion count.
+  const int nlist = min((int)gridDim.x, NLIST);
+  const int list = blockIdx.x % nlist;
+  const uint32_t count = list < total ? (uint32_t)((total - list + nlist - 1) / nlist) : 0u;
+  const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
+  uint32_t* ctr = reinterpret_cast<uint32_t*>(p.ctrl) + list * CTRL_STRIDE;
+  if (tid == 0) {
+    sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.salt = 0;
+    sm.item = atomicAdd(ctr, 1u) - sm.base;  // relative fetch index
+  }
+  __syncthreads();
+  const uint32_t base = sm.base;
+
+  // Publishes the fetched-ahead index to the workgroup and returns it.
+  auto advance = [&](uint32_t next) -> uint32_t {
     __syncthreads();
-    const int item = sm.item;
-    if (item >= total) break;
+    if (tid == 0) sm.item = next;
+    __syncthreads();
+    return sm.item;
+  };
+  // Row of relative index `rel`, or -1 past the end of the list.
+  auto resolve = [&](uint32_t rel) -> int {
+    if (rel >= count) return -1;
+    const int item = list + (int)rel * nlist;
     for (int r = tid; r < nrows; r += NT)
       if (sm.off[r] <= item && item < sm.off[r + 1]) sm.row = r;
     __syncthreads();
-    const int r = sm.row;
-    const int local = item - sm.off[r];
-    if (r < p.np) prefill_item<FP8, NQT>(p, sm, r, local);
-    else decode_item<FP8, NQT>(p, sm, r - p.np, local, item - decode_base);
-    __syncthreads();
-  }
+    return sm.row;
+  };
 
-  if (tid == 0) {
-    __threadfence();
-    if (atomicAdd(&p.ctrl[1], 1) == (int)gridDim.x - 1) {
-      atomicExch(&p.ctrl[0], 0);
-      atomicExch(&p.ctrl[1], 0);
+  uint32_t rel = sm.item;
+  __syncthreads();
+  int r = resolve(rel);
+  while (r >= 0) {
+    // sm.salt is always 0; reading it here keeps the lane-derived values of the
+    // two item paths from being hoisted out of the loop, where they would all
+    // stay live at once.
+    const int ltid = tid + sm.salt;
+    if (r < p.np) {
+      const int item = list + (int)rel * nlist;
+      uint32_t next = 0;
+      if (tid == 0) next = atomicAdd(ctr, 1u) - base;  // fetched ahead, consumed at the end
+      prefill_item<FP8>(p, sm, r, item - sm.off[r], ltid);
+      rel = advance(next);
+      r = resolve(rel);
+      continue;
+    }
+    // A run of decode items: the next item's loads are issued before the
+    // current item's merge tail, so HBM stays busy across items.
+    DecodeState st;
+    {
+      const int item = list + (int)rel * nlist;
+      decode_issue<FP8>(p, sm, st, r - p.np, item - sm.off[r], item - decode_base, ltid);
+    }
+    for (;;) {
+      uint32_t next = 0;
+      if (tid == 0) next = atomicAdd(ctr, 1u) - base;
+      f32x4 o[8];
+      float mx, ls;
+      decode_compute<FP8>(p, sm, st, ltid, o, mx, ls);
+      const int cb = st.b, chd = st.h, cc = st.c, cn = st.nch, cdi = st.dindex;
+      rel = advance(next);
+      r = resolve(rel);
+      const bool more = r >= p.np;
+      if (more) {
+        const int item = list + (int)rel * nlist;
+        decode_issue<FP8>(p, sm, st, r - p.np, item - sm.off[r], item - decode_base, ltid);
+      }
+      decode_tail(p, sm, cb, chd, cc, cn, cdi, ltid, o, mx, ls);
+      if (!more) break;
     }
   }
+  if (tid == 0 && sm.item == count + wgs - 1u)
+    __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-constexpr int kNQT = 2;  // 16-position column tiles per prefill wavefront
 
 struct DeviceShape {
   int cus = 0;
@@ -661,9 +827,9 @@ int device_shape(DeviceShape* out) {
     DeviceShape s;
     if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return fail(SLO_ERR_HIP, "hipDeviceGetAttribute failed");
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[0], paged_attention_kernel<false, kNQT>, NT, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[0], paged_attention_kernel<false>, NT, 0) !=
             hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[1], paged_attention_kernel<true, kNQT>, NT, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[1], paged_attention_kernel<true>, NT, 0) !=
             hipSuccess)
       return fail(SLO_ERR_HIP, "occupancy query failed");
     s.wg_per_cu[0] = std::max(1, s.wg_per_cu[0]);
@@ -705,7 +871,7 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   const bool do_pf = (a->phases & SLO_PHASE_PREFILL) && a->num_prefill > 0;
   if (a->num_decode < 0 || a->num_prefill < 0) return fail(SLO_ERR_INVALID, "paged_attention: negative row count");
   if ((do_dec ? a->num_decode : 0) + (do_pf ? a->num_prefill : 0) > MAX_ROWS)
-    return fail(SLO_ERR_UNSUPPORTED, "paged_attention: more than 2048 rows in one launch");
+    return fail(SLO_ERR_UNSUPPORTED, "paged_attention: more than 1024 rows in one launch");
   if (!do_dec && !do_pf) return SLO_OK;
   if (!a->q || !a->out || !a->workspace) return fail(SLO_ERR_INVALID, "paged_attention: null q/out/workspace");
   if ((a->q_row_stride % 8) || (a->out_row_stride % 8) || (reinterpret_cast<uintptr_t>(a->q) % 16) ||
@@ -789,7 +955,6 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   p.partials = reinterpret_cast<float*>(ws + PARTIALS_OFFSET);
 
   // Upper bound on the item count from host-known shapes only.
-  constexpr int BQ = 16 * kNQT;
   int64_t bound = 0;
   if (do_dec) bound += (int64_t)p.nd * ((dec_len_cap + CHUNK - 1) / CHUNK) * p.hkv;
   if (do_pf) {
@@ -799,7 +964,7 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8 ? 1 : 0];
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (fp8) hipLaunchKernelGGL((paged_attention_kernel<true, kNQT>), dim3(grid), dim3(NT), 0, s, p);
-  else hipLaunchKernelGGL((paged_attention_kernel<false, kNQT>), dim3(grid), dim3(NT), 0, s, p);
+  if (fp8) hipLaunchKernelGGL((paged_attention_kernel<true>), dim3(grid), dim3(NT), 0, s, p);
+  else hipLaunchKernelGGL((paged_attention_kernel<false>), dim3(grid), dim3(NT), 0, s, p);
   return check_launch("paged_attention");
 }

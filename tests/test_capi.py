@@ -40,7 +40,7 @@ def test_workspace_bytes_and_errors():
     # control words + ticket array are fixed; partials grow with rows x chunks x heads
     per_item = 4 * (128 + 2) * 4
     assert n2 - n1 == 24 * 16 * 8 * per_item
-    assert n0 == 256 + 4 * 65536
+    assert n0 == 8 * 128 + 4 * 65536
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.workspace_bytes(1, 1, 32, 8, 64)
     with pytest.raises(RuntimeError):
