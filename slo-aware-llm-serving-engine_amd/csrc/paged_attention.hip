@@ -65,6 +65,7 @@ constexpr int NQT = 2;                 // 16-position column tiles per prefill w
 constexpr int BQ = 16 * NQT;           // query positions per prefill item
 constexpr int MAX_ROWS = 1024;         // decode + prefill rows per launch
 constexpr int MAX_G = 16;              // query heads per kv head
+constexpr int MAX_PAGES = 256;         // prefill block-table entries cached in LDS
 constexpr int NLIST = 8;          // work lists (one per XCD)
 constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
 constexpr int CTRL_BYTES = NLIST * CTRL_STRIDE * 4;
@@ -125,6 +126,7 @@ struct Smem {
   } mg;                            // decode: cross-wavefront merge, 4 query heads per pass
   float ks[2][TT];
   float vs[2][TT];
+  int pages[MAX_PAGES];  // prefill: block table of the current row
   int off[MAX_ROWS + 1];
   int wsum[4];
   uint32_t item;
@@ -158,11 +160,12 @@ __device__ __forceinline__ s16x4 lds_tr16(const uint8_t* p) {
 }
 
 __device__ __forceinline__ bf16x8 join_tr(const s16x4& a, const s16x4& b) {
+  const u32x2 x = __builtin_bit_cast(u32x2, a), y = __builtin_bit_cast(u32x2, b);
   u32x4 r;
-  r.x = (uint32_t)(uint16_t)a[0] | ((uint32_t)(uint16_t)a[1] << 16);
-  r.y = (uint32_t)(uint16_t)a[2] | ((uint32_t)(uint16_t)a[3] << 16);
-  r.z = (uint32_t)(uint16_t)b[0] | ((uint32_t)(uint16_t)b[1] << 16);
-  r.w = (uint32_t)(uint16_t)b[2] | ((uint32_t)(uint16_t)b[3] << 16);
+  r.x = x.x;
+  r.y = x.y;
+  r.z = y.x;
+  r.w = y.y;
   return as_bf16x8(r);
 }
 
@@ -174,6 +177,78 @@ __device__ __forceinline__ bf16x8 vt_operand(const uint8_t* tile, int ks, int dt
   const int c = 2 * dt + ((n & 3) >> 1);
   const int half = (n & 1) << 3;
   return join_tr(lds_tr16(tile + v_off(r0, c) + half), lds_tr16(tile + v_off(r0 + 16, c) + half));
+}
+
+// max / sum over the 4 lanes {l, l^16, l^32, l^48} (one query column) with
+// v_permlane16_swap / v_permlane32_swap instead of LDS-crossbar shuffles.
+__device__ __forceinline__ float col_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Online-softmax update of one prefill tile for the wavefront's NQT query
+// columns.  Scores stay unscaled until the exponent: max commutes with the
+// positive factor c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA
+// and one v_exp_f32 per score.  MASK selects the boundary-tile path (keys past
+// the tile's valid rows or causally after the column).
+template <bool MASK>
+__device__ __forceinline__ void prefill_softmax(f32x4 (&s)[4][NQT], float (&m)[NQT], float (&l)[NQT],
+                                                f32x4 (&o)[8][NQT], bf16x8 (&pb)[NQT][2], float c, bool src_fp8,
+                                                const float* ks, const float* vs, int g, int ntok, int kv0,
+                                                int lim0) {
+#pragma unroll
+  for (int nt = 0; nt < NQT; ++nt) {
+    const int lim = lim0 + 16 * nt;  // last visible key index of this column
+    float mx = NEG_INF;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = 16 * mt + 4 * g + i;
+        float x = s[mt][nt][i];
+        if (src_fp8) x *= ks[tok];
+        if constexpr (MASK) x = (tok < ntok && kv0 + tok <= lim) ? x : NEG_INF;
+        s[mt][nt][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = col_max(mx);
+    const float mnew = fmaxf(m[nt], mx);
+    const float cm = mnew == NEG_INF ? 0.0f : c * mnew;
+    const float alpha = __builtin_amdgcn_exp2f(c * m[nt] - cm);
+    float rs = 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][i], c, -cm));
+        rs += e;
+        s[mt][nt][i] = src_fp8 ? e * vs[16 * mt + 4 * g + i] : e;
+      }
+    rs = col_sum(rs);
+    l[nt] = l[nt] * alpha + rs;
+    m[nt] = mnew;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // no column's max moved: skip the rescale
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
+    }
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      u32x4 w;
+      w.x = pack_bf16x2(s[2 * ks2][nt][0], s[2 * ks2][nt][1]);
+      w.y = pack_bf16x2(s[2 * ks2][nt][2], s[2 * ks2][nt][3]);
+      w.z = pack_bf16x2(s[2 * ks2 + 1][nt][0], s[2 * ks2 + 1][nt][1]);
+      w.w = pack_bf16x2(s[2 * ks2 + 1][nt][2], s[2 * ks2 + 1][nt][3]);
+      pb[nt][ks2] = as_bf16x8(w);
+    }
+  }
 }
 
 __device__ __forceinline__ int decode_len(const Params& p, int b) {
@@ -522,54 +597,76 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
   // compute.  Rows past the valid keys are zero.
   u32x4 kr[4], vr[4];
   float ksr = 0.0f, vsr = 0.0f;
+  const int* prow = p.ptab + (int64_t)r * p.ptab_stride;
+  const int npages = paged ? (kend + p.block_size - 1) / p.block_size : 0;
+  const bool cached = npages <= MAX_PAGES;
+  typedef __attribute__((address_space(3))) const int lds_int;
+  lds_int* pages = (lds_int*)(sm.pages);
+  // Lane-constant element offsets of this thread's 4 tile rows (row
+  // (tid>>4)+16*it, swizzled 16-byte chunk) from the tile's first key.
+  const int krow = paged ? p.hkv * HD : (int)p.k_stride;  // row strides < 2^25 elements (checked on the host)
+  const int vrow = paged ? p.hkv * HD : (int)p.v_stride;
+  int kgo[4], vgo[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int row = (tid >> 4) + 16 * it;
+    kgo[it] = row * krow + 8 * ((tid & 15) ^ (row & 15));
+    vgo[it] = row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1));
+  }
   auto issue_tile = [&](int kv0, int buf) {
     const int ntok = min(TT, kend - kv0);
     bool ok = true;
-    int64_t slot0 = 0;
+    int64_t slot0 = 0, kbase, vbase;  // element offsets of the tile's first key, head h
     if (paged) {
-      const int page = p.ptab[(int64_t)r * p.ptab_stride + kv0 / p.block_size];
+      const int page = cached ? pages[kv0 / p.block_size] : prow[kv0 / p.block_size];
       ok = page >= 0 && page < p.num_blocks;
       slot0 = ok ? (int64_t)page * p.block_size + kv0 % p.block_size : 0;
+      kbase = vbase = slot0 * p.hkv * HD + (int64_t)h * HD;
+    } else {
+      kbase = (int64_t)(k_start + kv0) * p.k_stride + (int64_t)h * HD;
+      vbase = (int64_t)(k_start + kv0) * p.v_stride + (int64_t)h * HD;
     }
     const int nv = ok ? ntok : 0;
+    if (src_fp8) {
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      const int kc = (tid & 15) ^ (row & 15);
-      const int vc = (tid & 15) ^ ((row & 7) << 1);
-      if (src_fp8) {
+      for (int it = 0; it < 4; ++it) {
+        const int row = (tid >> 4) + 16 * it;
         u32x4 kx = u32x4{0, 0, 0, 0}, vx = u32x4{0, 0, 0, 0};
         if (row < nv) {
-          const int64_t e = (slot0 + row) * (int64_t)p.hkv * HD + (int64_t)h * HD;
-          kx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.k_cache) + e + 8 * kc));
-          vx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + e + 8 * vc));
+          kx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.k_cache) + kbase + kgo[it]));
+          vx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + vbase + vgo[it]));
         }
         kr[it] = kx;
         vr[it] = vx;
-      } else if (row < nv) {
-        const uint16_t* ks;
-        const uint16_t* vs;
-        if (paged) {
-          const int64_t e = (slot0 + row) * (int64_t)p.hkv * HD + (int64_t)h * HD;
-          ks = static_cast<const uint16_t*>(p.k_cache) + e;
-          vs = static_cast<const uint16_t*>(p.v_cache) + e;
-        } else {
-          const int64_t tk = (int64_t)(k_start + kv0 + row);
-          ks = p.k + tk * p.k_stride + (int64_t)h * HD;
-          vs = p.v + tk * p.v_stride + (int64_t)h * HD;
-        }
-        __builtin_amdgcn_global_load_lds(ks + 8 * kc, sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vs + 8 * vc, sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+      }
+      if (tid < TT) {
+        const bool okt = tid < nv;
+        const int64_t si = (slot0 + tid) * p.hkv + h;
+        ksr = okt ? p.k_scale[si] : 0.0f;
+        vsr = okt ? p.v_scale[si] : 0.0f;
+      }
+      return;
+    }
+    const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
+    const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
+    if (nv == TT) {  // full tile: DMA only
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+      }
+      return;
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      if (row < nv) {
+        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
       } else {
         st16(sm.u.pf.k[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
         st16(sm.u.pf.v[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
       }
-    }
-    if (src_fp8 && tid < TT) {
-      const bool okt = tid < nv;
-      const int64_t si = (slot0 + tid) * p.hkv + h;
-      ksr = okt ? p.k_scale[si] : 0.0f;
-      vsr = okt ? p.v_scale[si] : 0.0f;
     }
   };
   auto commit_tile = [&](int buf) {  // register-staged (E4M3FN) tiles only
@@ -586,6 +683,18 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
     }
   };
 
+  // Lane-constant LDS byte offsets of the MFMA operands within a tile: K rows
+  // 16mt+n (mt added per use), V^T rows 32ks + 4g + n/4 (+16 for slots 4-7).
+  int koff[4], voff[8];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) koff[st] = k_off(n, 4 * st + g);
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) voff[dt] = v_off(4 * g + (n >> 2), 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3);
+
+  // The row's block table goes to LDS once, so no tile waits on a table load.
+  if (cached)
+    for (int i = tid; i < npages; i += NT) sm.pages[i] = prow[i];
+  __syncthreads();
   if (kend > 0) {
     issue_tile(0, 0);
     commit_tile(0);
@@ -601,79 +710,42 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
       const uint8_t* kt = sm.u.pf.k[buf];
       const uint8_t* vt = sm.u.pf.v[buf];
 
+      // S^T = K Q^T; the next K fragment is read while the current one feeds the MFMAs.
       f32x4 s[4][NQT];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        u32x4 kf[4];
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int st = 0; st < 4; ++st) kf[st] = ld16(kt + k_off(16 * mt + n, 4 * st + g));
+        for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = f32x4{0, 0, 0, 0};
+      u32x4 kf = ld16(kt + koff[0]);
 #pragma unroll
-        for (int nt = 0; nt < NQT; ++nt) {
-          f32x4 acc = f32x4{0, 0, 0, 0};
+      for (int i = 0; i < 16; ++i) {  // i = 4*mt + st
+        const int mt = i >> 2, st = i & 3;
+        const u32x4 kn = i + 1 < 16 ? ld16(kt + ((i + 1) >> 2) * 16 * ROWB + koff[(i + 1) & 3]) : kf;
 #pragma unroll
-          for (int st = 0; st < 4; ++st) acc = mfma16(as_bf16x8(kf[st]), as_bf16x8(qv[nt][st]), acc);
-          s[mt][nt] = acc;
-        }
+        for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = mfma16(as_bf16x8(kf), as_bf16x8(qv[nt][st]), s[mt][nt]);
+        kf = kn;
       }
 
       // Keys that can be masked: beyond the tile's valid rows, or causally
       // after the earliest query column of the block.
       const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
       bf16x8 pb[NQT][2];
-#pragma unroll
-      for (int nt = 0; nt < NQT; ++nt) {
-        const int lim = q0 + 16 * nt + n + prefix;  // last visible key index of this column
-        float mx = NEG_INF;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int tok = 16 * mt + 4 * g + i;
-            float x = s[mt][nt][i] * p.scale_log2;
-            if (src_fp8) x *= sm.ks[buf][tok];
-            if (need_mask) x = (tok < ntok && kv0 + tok <= lim) ? x : NEG_INF;
-            s[mt][nt][i] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = wave_max_xor(mx, 16);
-        mx = wave_max_xor(mx, 32);
-        const float mnew = fmaxf(m[nt], mx);
-        const float mu = mnew == NEG_INF ? 0.0f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m[nt] - mu);
-        float rs = 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(s[mt][nt][i] - mu);
-            rs += e;
-            s[mt][nt][i] = src_fp8 ? e * sm.vs[buf][16 * mt + 4 * g + i] : e;
-          }
-        rs += __shfl_xor(rs, 16, 64);
-        rs += __shfl_xor(rs, 32, 64);
-        l[nt] = l[nt] * alpha + rs;
-        m[nt] = mnew;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          u32x4 w;
-          w.x = pack_bf16x2(s[2 * ks][nt][0], s[2 * ks][nt][1]);
-          w.y = pack_bf16x2(s[2 * ks][nt][2], s[2 * ks][nt][3]);
-          w.z = pack_bf16x2(s[2 * ks + 1][nt][0], s[2 * ks + 1][nt][1]);
-          w.w = pack_bf16x2(s[2 * ks + 1][nt][2], s[2 * ks + 1][nt][3]);
-          pb[nt][ks] = as_bf16x8(w);
-        }
-      }
+      const int lim0 = q0 + n + prefix;
+      prefill_softmax<true>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.ks[buf], sm.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
 
+      // O^T += V^T P^T; the next V^T operand is read while the current one feeds the MFMAs.
+      auto vload = [&](int i) {
+        const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
+        return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
+      };
+      bf16x8 va = vload(0);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int i = 0; i < 16; ++i) {
+        const bf16x8 vn = i + 1 < 16 ? vload(i + 1) : va;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const bf16x8 va = vt_operand(vt, ks, dt, g, n);
-#pragma unroll
-          for (int nt = 0; nt < NQT; ++nt) o[dt][nt] = mfma16(va, pb[nt][ks], o[dt][nt]);
-        }
+        for (int nt = 0; nt < NQT; ++nt) o[i & 7][nt] = mfma16(va, pb[nt][i >> 3], o[i & 7][nt]);
+        va = vn;
+      }
     }
     if (more) commit_tile(buf ^ 1);
   }
@@ -899,7 +971,8 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
       if (a->prefill_table_width <= 0 || a->prefill_table_stride < a->prefill_table_width)
         return fail(SLO_ERR_INVALID, "paged_attention: bad prefill tables");
     } else {
-      if (!a->k || !a->v || (a->k_row_stride % 8) || (a->v_row_stride % 8) ||
+      if (!a->k || !a->v || (a->k_row_stride % 8) || (a->v_row_stride % 8) || a->k_row_stride >= (1 << 25) ||
+          a->v_row_stride >= (1 << 25) ||
           (reinterpret_cast<uintptr_t>(a->k) % 16) || (reinterpret_cast<uintptr_t>(a->v) % 16))
         return fail(SLO_ERR_INVALID, "paged_attention: contiguous K/V must be 16-byte aligned bf16 rows");
     }
