@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16")
     ap.add_argument("--events", type=int, default=100, help="event-timed launches per mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile", choices=["fused", "decode", "prefill"], default=None,
+                    help="only launch this attention phase (for rocprofv3 counter runs), plus one "
+                         "256 MiB device copy whose counters calibrate FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -102,6 +105,26 @@ def main():
             prefill_tables=meta.prefill_tables, phases=phases, out=out_buf)
 
     out_buf = torch.empty_like(q)
+    if args.profile:
+        phase = {"fused": _lib.PHASE_ALL, "decode": _lib.PHASE_DECODE, "prefill": _lib.PHASE_PREFILL}[args.profile]
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+        times = []
+        for i in range(args.warmup + args.events):
+            torch.cuda._sleep(200_000)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            attn_only(i, phase)
+            e1.record()
+            e1.synchronize()
+            if i >= args.warmup:
+                times.append(e0.elapsed_time(e1) * 1e3)
+        print(json.dumps({"profile": args.profile, "launches": args.warmup + args.events,
+                          "avg_launch_us": round(statistics.mean(times), 2),
+                          "median_launch_us": round(statistics.median(times), 2)}))
+        return
     for i in range(max(args.warmup, 4)):
         step(i)
     torch.cuda.synchronize()
@@ -165,6 +188,14 @@ def main():
     dec_gbs = (dec_bytes + 2 * w.num_decode * hq * d * 2) / (t_dec * 1e-6) / 1e9
     pre_tflops = flops / (t_pre * 1e-6) / 1e12
 
+    # HBM bytes per fused launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE,
+    # calibrated against a 256 MiB copy) for this kernel, kept under profiles/.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_mixed_24decode_2x512chunk.json")
+    if not fp8 and os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = round(json.load(fh)["fused"]["traffic_mb"] * 1e6)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, fp8)
@@ -190,7 +221,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(fused_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "paged_attention_kernel (fused decode+prefill)",
             "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(t_fused, 2),
             "median_launch_us": round(t_fused_med, 2),
