@@ -56,11 +56,16 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
     args.head_dim, args.num_heads = 128, 31
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 1
-    args.num_heads, args.block_size, args.kv_dtype = 32, 100, 0
-    assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
+    args.num_heads, args.kv_dtype = 32, 0
     # nothing to do -> OK with no device work
-    args.block_size = 256
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 0
+    # a pooled decode row with a block size that is not a multiple of 64 is refused
+    # before any pointer is touched (the pointers below are never dereferenced)
+    args.num_decode, args.num_q_rows, args.block_size, args.num_blocks = 1, 1, 100, 1
+    args.q = args.out = args.k_cache = args.v_cache = 4096
+    args.workspace = 8192
+    assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
+    assert "block_size" in lib.slo_last_error().decode()
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 0, 8, 128, 0, None, None, None, None, 0, 1.0, None) == 0
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 4, 8, 96, 0, None, None, None, None, 0, 1.0, None) == 4
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 4, 8, 128, 0, None, None, None, None, 0, 1.0, None) == 1
