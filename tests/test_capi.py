@@ -61,7 +61,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 0
     # a pooled decode row with a block size that is not a multiple of 64 is refused
     # before any pointer is touched (the pointers below are never dereferenced)
-    args.num_decode, args.num_q_rows, args.block_size, args.num_blocks = 1, 1, 100, 1
+    args.num_decode, args.num_q_rows, args.block_size, args.num_blocks, args.phases = 1, 1, 100, 1, 3
     args.q = args.out = args.k_cache = args.v_cache = 4096
     args.workspace = 8192
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
