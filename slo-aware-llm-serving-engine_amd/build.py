@@ -23,6 +23,10 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     # Packed fp32 VALU forms are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Work-list fetches and split-K tickets are single-lane atomics whose
+    # results are consumed late on purpose; the atomic optimizer's wave-level
+    # rewrite would read them back immediately and stall the loads in flight.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 

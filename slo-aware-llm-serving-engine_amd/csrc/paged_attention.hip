@@ -22,23 +22,24 @@
 //    lane-local: the S^T accumulator is the B operand of the PV product
 //    without data movement, and V^T comes from the natural [token][d] LDS tile
 //    through ds_read_b64_tr_b16.
-//  * Decode item (row b, chunk of 256 tokens, kv head h): each wavefront takes
-//    64 tokens; the G query heads sharing h are the MFMA columns, K goes from
-//    HBM straight into MFMA A-operand registers, V goes from HBM straight into
-//    LDS (global_load_lds_dwordx4) for the transposed read.  The 4 wavefronts
-//    merge in LDS; a row with several chunks writes one (m, l, acc) partial per
-//    chunk and the last chunk to finish merges them (the split-K merge of
-//    docs/project_manual.md:643-650).
+//  * Decode item (row b, chunk of 128 tokens, kv head h): two workgroup steps
+//    of 64 tokens, 16 per wavefront; the G query heads sharing h are the MFMA
+//    columns.  K, V and Q go from HBM straight into LDS (global_load_lds) and
+//    two steps stay in flight per wavefront across item boundaries.  The 4
+//    wavefronts merge in LDS; a row with several chunks writes one
+//    (acc, m, l) partial per chunk, and after its own items every workgroup
+//    takes split-K merge tasks from its list, each waiting for the chunks of
+//    its (row, head) (the split-K merge of docs/project_manual.md:643-650).
 //
 // LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
 // XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 2*(row & 7)), so the MFMA
 // operand reads of 16 lanes fall on distinct banks.
 //
 // Split-K visibility across XCDs: partials are written and read with
-// agent-scope atomic stores/loads (global_store/load ... sc1), which bypass
-// the per-XCD L2; each writer waits for its stores to be acknowledged
-// (s_waitcnt vmcnt(0)) and the workgroup barrier orders them before the
-// ticket increment.  No L2 writeback or invalidate is needed.
+// agent-scope stores/loads (global_store/load ... sc1), which bypass the
+// per-XCD L2; each writer waits for its stores to be acknowledged and a
+// workgroup barrier orders them before the ticket increment.  No L2 writeback
+// or invalidate is needed.
 //
 // Softmax runs in the log2 domain (scores scaled by softmax_scale*log2(e),
 // exp2 on v_exp_f32).  Fully-masked tiles never produce exp(-inf - -inf).
@@ -58,7 +59,7 @@ namespace slo {
 constexpr int HD = 128;                // head_dim this kernel implements
 constexpr int NT = 256;                // threads per workgroup (4 wavefronts)
 constexpr int TT = 64;                 // tokens per tile
-constexpr int CHUNK = 4 * TT;          // decode split-K chunk
+constexpr int CHUNK = 128;             // decode split-K chunk (tokens)
 constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
 constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
 constexpr int NQT = 2;                 // 16-position column tiles per prefill wavefront
@@ -68,8 +69,10 @@ constexpr int MAX_G = 16;              // query heads per kv head
 constexpr int MAX_PAGES = 256;         // prefill block-table entries cached in LDS
 constexpr int NLIST = 8;          // work lists (one per XCD)
 constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
-constexpr int CTRL_BYTES = NLIST * CTRL_STRIDE * 4;
+// Control words: one line per work list, then one per split-K merge-task list.
+constexpr int CTRL_BYTES = 2 * NLIST * CTRL_STRIDE * 4;
 constexpr int MAX_COUNTERS = 65536;
+constexpr int PREC = HD + 4;      // floats per query head in a split-K partial: acc[HD], m, l, 2 pad
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -111,28 +114,30 @@ struct Params {
   float* partials;
 };
 
+// The two tile stages live in two separate __shared__ arrays of STAGE_BYTES
+// (prefill: [K tile | V tile] of one buffer; decode: one DT-row V tile per
+// wavefront).  Separate objects let the compiler see that a transposed LDS
+// read of one stage cannot alias an LDS DMA still in flight to the other, so
+// it does not drain the vector memory counter before that read.
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+
 struct Smem {
   union {
-    uint8_t dec_v[4][TILE_BYTES];  // decode: one V tile per wavefront
     struct {
-      uint8_t k[2][TILE_BYTES];
-      uint8_t v[2][TILE_BYTES];
-    } pf;                          // prefill: double-buffered K/V tiles
+      float m[4][4];  // per wavefront, 4 query heads per pass
+      float l[4][4];
+    } dec;            // decode: cross-wavefront merge statistics
+    struct {
+      float ks[2][TT];
+      float vs[2][TT];
+      int pages[MAX_PAGES];  // block table of the current row
+    } pf;                    // prefill
   } u;
-  struct {
-    float o[4][4][HD];
-    float m[4][4];
-    float l[4][4];
-  } mg;                            // decode: cross-wavefront merge, 4 query heads per pass
-  float ks[2][TT];
-  float vs[2][TT];
-  int pages[MAX_PAGES];  // prefill: block table of the current row
   int off[MAX_ROWS + 1];
   int wsum[4];
   uint32_t item;
   uint32_t base;
   int row;
-  int last;
   int salt;
 };
 
@@ -273,273 +278,527 @@ __device__ __forceinline__ float load_partial(const float* p) {
 }
 
 // ---------------------------------------------------------------- decode item
-// A decode item is split in three steps so that the next item's HBM loads can
-// be in flight while the current item finishes: issue (metadata, Q/K loads to
-// registers, V HBM -> LDS), compute (QK, softmax, PV into registers) and tail
-// (cross-wavefront merge, split-K partial / ticket / final merge, output).
-struct DecodeState {
-  int b, h, c, nch, ntok, dindex;
-  int64_t slot0;
-  u32x4 qv[4];
-  u32x4 k[4][4];   // bf16 K operand (bf16 pool)
-  u32x2 k8[4][4];  // raw E4M3FN K bytes (E4M3FN pool)
-  u32x2 vraw[16];  // raw E4M3FN V rows (bf16 V goes straight to LDS)
-  float ksc, vsc;  // E4M3FN scales of token `lane` of this wavefront's tile
+// A decode item (row b, kv head h, chunk c of CHUNK tokens) is two workgroup
+// steps of DSTEP tokens; in step s wavefront w takes the DT tokens starting at
+// c*CHUNK + s*DSTEP + w*DT.  A workgroup step lies in one KV block (block_size
+// is a multiple of 64).  Step s always uses LDS stage s, and the Q of the item
+// goes to its own LDS array, so K, V and Q all go HBM -> LDS through
+// global_load_lds_dwordx4 and no streamed data is held in registers across
+// iterations.  Every wait for the streamed data is an explicit
+// `s_waitcnt vmcnt(D_GROUP)`: vector memory operations complete in issue
+// order, and when a step is consumed exactly one later group of D_GROUP loads
+// has been issued after everything it needs.  Two steps are in flight per
+// wavefront at all times, across item boundaries.
+//
+// Each step issues the same number of loads: lanes past the row's length read
+// valid rows of the same block (slot 0 of the pool when the block is padding)
+// and are masked afterwards; after the last item the next-item loads repeat
+// the current item's (drained before the run ends).  Split-K partials are
+// written by wavefront 0 after the cross-wavefront merge and are complete at
+// the next item's first wait, where the ticket is taken; its result (and the
+// work-list fetch issued beside it) is read after the second wait of that
+// item, so no wait ever covers loads issued for a later step.
+//
+// Inside the decode loop every vector memory operation (LDS DMA, atomics,
+// split-K and output stores) is issued through inline assembly, so the
+// compiler inserts no vector-memory waits of its own there: its bookkeeping
+// cannot follow loads that land in LDS and would drain the pipeline.  The
+// results of the two atomics are only read after an explicit wait that covers
+// them, through an empty asm that ties the value to that point.
+constexpr int DT = 16;                 // tokens per wavefront step
+constexpr int DSTEP = 4 * DT;          // tokens per workgroup step
+constexpr int WSTAGE = 2 * DT * ROWB;  // per wavefront and stage: K rows, then V rows (bf16)
+static_assert(CHUNK == 2 * DSTEP, "a decode item is two workgroup steps");
+static_assert(4 * WSTAGE <= STAGE_BYTES, "decode stage must fit the tile stage");
+
+// Loads of one wavefront step: K and V (4 + 4 bf16 DMA, or 2 + 2 E4M3FN DMA
+// plus one DMA of the 32 scales).
+template <bool FP8>
+__device__ __forceinline__ constexpr int d_group() { return FP8 ? 5 : 8; }
+
+// s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// LDS byte address of a pointer into a __shared__ array (wave-uniform).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+
+// global -> LDS DMA: lane i's 16 (or 4) bytes at gp land at LDS lds + 16i (4i).
+__device__ __forceinline__ void dma16(const void* gp, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* gp, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
+}
+// Atomic add returning the old value; the value is valid only after a wait
+// that covers this operation.
+__device__ __forceinline__ uint32_t atomic_add_ret(void* p, uint32_t v) {
+  uint32_t r;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(r) : "v"(p), "v"(v) : "memory");
+  return r;
+}
+__device__ __forceinline__ void atomic_add_noret(void* p, uint32_t v) {
+  asm volatile("global_atomic_add %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+// Stores: agent-scope (write-through to the coherence point) for split-K
+// partials, plain for outputs.
+__device__ __forceinline__ void store16_agent(void* p, const u32x4& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store8_agent(void* p, const u32x2& v) {
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store4(void* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+// Ties x to this point: uses of x cannot move above an earlier wait.
+__device__ __forceinline__ uint32_t after_wait(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Scalar (SMEM) loads of read-only metadata at wave-uniform addresses: they are
+// counted by lgkmcnt, so they never order against the KV loads in flight.
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+__device__ __forceinline__ int sload(const int32_t* base, int64_t i) { return ((const_i32*)base)[i]; }
+
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits
+// for every LDS DMA write still in flight (vmcnt), which would drain the KV
+// loads; the decode stages are private to their wavefront, so the barriers of
+// the decode loop (Q, merge area, item broadcast) need only the LDS counter.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+struct DMeta {
+  int b, h, c, dindex;  // wave-uniform
+  int len;              // dlens[b] as read (clamped where used)
+  int page[2];          // KV block of workgroup step 0 and 1
 };
 
+// The SMEM results (len, page) are used only where needed, so their latency
+// stays hidden behind the item ahead of them.
+__device__ __forceinline__ int decode_L(const Params& p, const DMeta& m) {
+  return min(max(m.len, 0), p.dtab_width * p.block_size);
+}
+__device__ __forceinline__ int decode_nch(const Params& p, const DMeta& m) {
+  return max(1, (decode_L(p, m) + CHUNK - 1) / CHUNK);
+}
+
+__device__ __forceinline__ DMeta decode_meta(const Params& p, const Smem& sm, int item, int r, int decode_base) {
+  DMeta m;
+  r = __builtin_amdgcn_readfirstlane(r);
+  item = __builtin_amdgcn_readfirstlane(item);
+  m.b = r - p.np;
+  const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
+  m.h = local % p.hkv;
+  m.c = local / p.hkv;
+  m.len = sload(p.dlens, m.b);
+  m.dindex = item - decode_base;
+  // Block-table entries are read here, an item ahead of their use.
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int t0 = m.c * CHUNK + s * DSTEP;
+    m.page[s] = sload(p.dtab, (int64_t)m.b * p.dtab_stride + min(t0 / p.block_size, p.dtab_width - 1));
+  }
+  return m;
+}
+
+// Row of item `item` among rows [lo, nrows), searched by one wavefront.
+__device__ __forceinline__ int find_row(const Smem& sm, int item, int lo, int nrows, int lane) {
+  for (int base = lo; base < nrows; base += 64) {
+    const int r = base + lane;
+    const bool hit = r < nrows && sm.off[r] <= item && item < sm.off[r + 1];
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(hit);
+    if (mask) return base + (int)__builtin_ctzll(mask);
+  }
+  return -1;
+}
+
+// Valid tokens of wavefront `wave` in step s of the item (0 for padding blocks).
+__device__ __forceinline__ int decode_ntok(const Params& p, const DMeta& m, int s, int wave) {
+  const int page = m.page[s];
+  if (page < 0 || page >= p.num_blocks) return 0;
+  return min(max(decode_L(p, m) - (m.c * CHUNK + s * DSTEP + wave * DT), 0), DT);
+}
+
+// The item's G query heads (G*HD bf16, contiguous in the row) to qbuf; each
+// wavefront copies one quarter.
+__device__ __forceinline__ void decode_issue_q(const Params& p, uint8_t* qbuf, const DMeta& m, int wave, int lane) {
+  const int qb = 64 * p.G;  // bytes per wavefront
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(p.q + (int64_t)m.b * p.q_stride + (int64_t)m.h * p.G * HD);
+  const uint32_t dst = lds_addr(qbuf + wave * qb);
+  if (lane < 4 * p.G) dma16(src + wave * qb + 16 * lane, dst);
+}
+
+// K and V of one wavefront step to the wavefront's stage region `stg`.
+// bf16: K row r at r*ROWB with 16-byte chunk c in slot c ^ (r & 15), V rows
+// from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN: K codes (128 B
+// rows, chunk c in slot c ^ (r & 7)) at 0, V codes likewise at 2048, K scales
+// at 4096 and V scales at 4160.
 template <bool FP8>
-__device__ __forceinline__ void decode_issue(const Params& p, Smem& sm, DecodeState& st, int b, int local,
-                                             int dindex, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, const DMeta& m, int s, int wave,
+                                             int lane) {
   const int n = lane & 15, g = lane >> 4;
-  const int G = p.G;
-  st.b = b;
-  st.h = local % p.hkv;
-  st.c = local / p.hkv;
-  st.dindex = dindex;
-  const int L = decode_len(p, b);
-  st.nch = max(1, (L + CHUNK - 1) / CHUNK);
-  const int t0 = st.c * CHUNK + wave * TT;
-  int ntok = min(max(L - t0, 0), TT);
-  int64_t slot0 = 0;
-  if (ntok > 0) {
-    const int page = p.dtab[(int64_t)b * p.dtab_stride + t0 / p.block_size];
-    if (page < 0 || page >= p.num_blocks) ntok = 0;  // never dereference padding
-    else slot0 = (int64_t)page * p.block_size + (t0 % p.block_size);
-  }
-  st.ntok = ntok;
-  st.slot0 = slot0;
-  const int64_t tok_stride = (int64_t)p.hkv * HD;
-  const int64_t head_off = (int64_t)st.h * HD;
-  uint8_t* vt = sm.u.dec_v[wave];
-
-  // V tile: row r holds token t0 + r; rows past ntok are zeroed.
+  const int ntok = decode_ntok(p, m, s, wave);
+  const int t0 = m.c * CHUNK + s * DSTEP + wave * DT;
+  const int64_t slot0 = ntok > 0 ? (int64_t)m.page[s] * p.block_size + t0 % p.block_size : 0;
+  const int row = p.hkv * HD;  // elements (bf16) or bytes (E4M3FN) between tokens
+  const int64_t base = slot0 * row + (int64_t)m.h * HD;
   if constexpr (!FP8) {
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + slot0 * tok_stride + head_off;
+    const uint16_t* kc = static_cast<const uint16_t*>(p.k_cache) + base;
+    const uint16_t* vc = static_cast<const uint16_t*>(p.v_cache) + base;
+    const uint32_t dst = lds_addr(stg);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = 4 * i + g;  // == lane / 16 within this 4-row stripe
-      const int chunk = n ^ ((r & 7) << 1);
-      if (r < ntok) __builtin_amdgcn_global_load_lds(vbase + r * tok_stride + 8 * chunk, vt + i * 1024, 16, 0, 0);
-      else st16(vt + r * ROWB + (n << 4), u32x4{0, 0, 0, 0});
-    }
-  } else {
-    const uint8_t* vbase = static_cast<const uint8_t*>(p.v_cache) + slot0 * tok_stride + head_off;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      const int chunk = n ^ ((r & 7) << 1);
-      st.vraw[i] = r < ntok ? ld8(vbase + r * tok_stride + 8 * chunk) : u32x2{0, 0};
+      dma16(kc + r * row + 8 * (n ^ (r & 15)), dst + i * 1024);
     }
-  }
-
-  // Q as the B operand: column n is query head h*G+n; k slot (g, st, j) is d = 8(4st+g)+j.
-  if (n < G) {
-    const uint16_t* qr = p.q + (int64_t)b * p.q_stride + (int64_t)(st.h * G + n) * HD;
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) st.qv[s4] = ld16(qr + 8 * (4 * s4 + g));
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + g;
+      dma16(vc + r * row + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
+    }
   } else {
+    const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
+    const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + base;
+    const uint32_t dst = lds_addr(stg);
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) st.qv[s4] = u32x4{0, 0, 0, 0};
-  }
-
-  // K as the A operand: row (token) 16mt+n, same k slots.
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int tok = 16 * mt + n;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const int64_t e = (slot0 + tok) * tok_stride + head_off + 8 * (4 * s4 + g);
-      if constexpr (FP8) {
-        st.k8[mt][s4] = tok < ntok ? ld8(static_cast<const uint8_t*>(p.k_cache) + e) : u32x2{0, 0};
-      } else {
-        st.k[mt][s4] = tok < ntok ? ld16(static_cast<const uint16_t*>(p.k_cache) + e) : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < 2; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
     }
-  }
-
-  if constexpr (FP8) {
-    const bool ok = lane < ntok;
-    const int64_t si = (slot0 + lane) * p.hkv + st.h;
-    st.ksc = ok ? p.k_scale[si] : 0.0f;
-    st.vsc = ok ? p.v_scale[si] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
+    }
+    // Lanes 0-15: K scales of the 16 tokens, lanes 16-31: V scales (lanes
+    // 32-63 repeat them into unused bytes).
+    const float* sc = (lane & 16) ? p.v_scale : p.k_scale;
+    dma4(sc + (slot0 + (lane & 15)) * p.hkv + m.h, dst + 4096);
   }
 }
 
-// QK, softmax and PV of the issued item.  Leaves this wavefront's O^T
-// accumulators (lane (n, g): head n, d = 16dt + 4g + i), its max and its sum.
+// QK, online softmax and PV of one landed step into this wavefront's running
+// (o, m, l); lane (n, g) holds O^T[d = 16dt + 4g + i][head n] and the
+// statistics of head n.  Scores are in the log2 domain.
 template <bool FP8>
-__device__ __forceinline__ void decode_compute(const Params& p, Smem& sm, DecodeState& st, int tid, f32x4 (&o)[8],
-                                               float& mx_out, float& ls_out) {
-  const int lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int ntok, const u32x4 (&qv)[4],
+                                            f32x4 (&o)[8], float& m, float& l, int lane) {
   const int n = lane & 15, g = lane >> 4;
-  const int ntok = st.ntok;
-  uint8_t* vt = sm.u.dec_v[wave];
+  uint8_t* vt = FP8 ? stg : stg + DT * ROWB;  // bf16 V tile (E4M3FN: decoded over the code bytes)
+
+  // S^T = K Q^T for the 16 tokens: k-step kk covers d = 32kk + 8g + {0..7}.
+  f32x4 s = f32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    u32x4 a;
+    if constexpr (FP8) {
+      const int c = 2 * kk + (g >> 1);
+      a = fp8x8_to_bf16x8(ld8(stg + n * 128 + 16 * (c ^ (n & 7)) + 8 * (g & 1)));
+    } else {
+      a = ld16(stg + k_off(n, 4 * kk + g));
+    }
+    s = mfma16(as_bf16x8(a), as_bf16x8(qv[kk]), s);
+  }
+
   if constexpr (FP8) {
+    // V codes -> bf16 tile over the code bytes: lane covers row lane/4, 32 bytes
+    // (d = 32*(lane%4)..+31).  All code reads of the wavefront are issued before
+    // its writes, and LDS executes a wavefront's accesses in order.
+    const int r = lane >> 2, seg = lane & 3;
+    u32x4 w0 = ld16(stg + 2048 + r * 128 + 16 * ((2 * seg) ^ (r & 7)));
+    u32x4 w1 = ld16(stg + 2048 + r * 128 + 16 * ((2 * seg + 1) ^ (r & 7)));
+    if (r >= ntok) w0 = w1 = u32x4{0, 0, 0, 0};
+    st16(vt + v_off(r, 4 * seg + 0), fp8x8_to_bf16x8(u32x2{w0.x, w0.y}));
+    st16(vt + v_off(r, 4 * seg + 1), fp8x8_to_bf16x8(u32x2{w0.z, w0.w}));
+    st16(vt + v_off(r, 4 * seg + 2), fp8x8_to_bf16x8(u32x2{w1.x, w1.y}));
+    st16(vt + v_off(r, 4 * seg + 3), fp8x8_to_bf16x8(u32x2{w1.z, w1.w}));
+  } else if (ntok < DT) {
+    // Rows past the valid tokens become zeros (the step has landed).
 #pragma unroll
-    for (int i = 0; i < 16; ++i) st16(vt + (4 * i + g) * ROWB + (n << 4), fp8x8_to_bf16x8(st.vraw[i]));
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) st.k[mt][s4] = fp8x8_to_bf16x8(st.k8[mt][s4]);
+    for (int i = 0; i < 4; ++i)
+      if (4 * i + g >= ntok) st16(vt + (4 * i + g) * ROWB + (n << 4), u32x4{0, 0, 0, 0});
   }
 
-  // S^T = K Q^T for the wavefront's 64 tokens.
-  f32x4 s[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    s[mt] = f32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) s[mt] = mfma16(as_bf16x8(st.k[mt][s4]), as_bf16x8(st.qv[s4]), s[mt]);
+  f32x4 ksc = f32x4{1, 1, 1, 1}, vsc = f32x4{1, 1, 1, 1};
+  if constexpr (FP8) {
+    ksc = __builtin_bit_cast(f32x4, ld16(stg + 4096 + 16 * g));
+    vsc = __builtin_bit_cast(f32x4, ld16(stg + 4160 + 16 * g));
   }
-
+  float x[4];
   float mx = NEG_INF;
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = 16 * mt + 4 * g + i;
-      float x = s[mt][i] * p.scale_log2;
-      if constexpr (FP8) x *= __shfl(st.ksc, tok, 64);
-      x = tok < ntok ? x : NEG_INF;
-      s[mt][i] = x;
-      mx = fmaxf(mx, x);
-    }
-  mx = wave_max_xor(mx, 16);
-  mx = wave_max_xor(mx, 32);
-  const float mu = mx == NEG_INF ? 0.0f : mx;
-  float ls = 0.0f;
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = __builtin_amdgcn_exp2f(s[mt][i] - mu);
-      ls += e;
-      if constexpr (FP8) s[mt][i] = e * __shfl(st.vsc, 16 * mt + 4 * g + i, 64);
-      else s[mt][i] = e;
-    }
-  ls += __shfl_xor(ls, 16, 64);
-  ls += __shfl_xor(ls, 32, 64);
-
-  // P^T as the B operand of O^T = V^T P^T; k slot (g, j) is token 32ks + 16(j/4) + 4g + j%4.
-  bf16x8 pb[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    u32x4 w;
-    w.x = pack_bf16x2(s[2 * ks][0], s[2 * ks][1]);
-    w.y = pack_bf16x2(s[2 * ks][2], s[2 * ks][3]);
-    w.z = pack_bf16x2(s[2 * ks + 1][0], s[2 * ks + 1][1]);
-    w.w = pack_bf16x2(s[2 * ks + 1][2], s[2 * ks + 1][3]);
-    pb[ks] = as_bf16x8(w);
+  for (int i = 0; i < 4; ++i) {
+    float v = s[i] * p.scale_log2;
+    if constexpr (FP8) v *= ksc[i];
+    x[i] = 4 * g + i < ntok ? v : NEG_INF;
+    mx = fmaxf(mx, x[i]);
   }
-
-  // The V tile (LDS DMA, zero rows or decoded E4M3FN rows) must have landed.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  mx = col_max(mx);
+  const float mnew = fmaxf(m, mx);
+  const float mu = mnew == NEG_INF ? 0.0f : mnew;
+  const float alpha = __builtin_amdgcn_exp2f(m - mu);
+  float e[4], rs = 0.0f;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
+  for (int i = 0; i < 4; ++i) {
+    e[i] = __builtin_amdgcn_exp2f(x[i] - mu);
+    rs += e[i];
+    if constexpr (FP8) e[i] *= vsc[i];
+  }
+  rs = col_sum(rs);
+  l = l * alpha + rs;
+  m = mnew;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+  }
+  // P^T as the B operand of the 16x16x16 product: k slot (g, j) is token 4g + j.
+  const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])});
+  // V^T operand: source lane n of group g reads row 4g + n/4, d = 16dt + 4(n%4).
+  const int r0 = 4 * g + (n >> 2);
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = mfma16(vt_operand(vt, ks, dt, g, n), pb[ks], o[dt]);
-  mx_out = mx;
-  ls_out = ls;
+  for (int dt = 0; dt < 8; ++dt) {
+    const s16x4 va = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
+    o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
+  }
 }
 
-// Cross-wavefront merge through LDS, then either the output (single chunk) or
-// the split-K partial + ticket, and the final merge by the last chunk.
-__device__ __forceinline__ void decode_tail(const Params& p, Smem& sm, int b, int h, int c, int nch, int dindex,
-                                            int tid, const f32x4 (&o)[8], float mx, float ls) {
+// Cross-wavefront merge.  Per pass of 4 query heads, every wavefront writes
+// its accumulators into its own stage-1 region (idle between its last step
+// and the next item's step-1 loads) and its (m, l) into the merge area; after
+// a barrier, wavefront w combines query head 4*pass + w over the four
+// wavefronts and writes the output (single chunk) or the chunk's split-K
+// partial.  Entered after a barrier that follows every wavefront's last step;
+// ends with a barrier, after which the stage-1 regions may take new loads.
+__device__ __forceinline__ void decode_merge(const Params& p, Smem& sm, uint8_t* st1, const DMeta& md, int tid,
+                                             const f32x4 (&o)[8], float mx, float ls) {
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int G = p.G;
-  float* part = p.partials + (size_t)dindex * G * (HD + 2);
-  for (int hg = 0; hg < G; hg += 4) {  // 4 query heads per pass through the merge area
-    __syncthreads();
+  const int nch = decode_nch(p, md);
+  float* part = p.partials + (size_t)md.dindex * G * PREC;
+  float* own = reinterpret_cast<float*>(st1 + wave * WSTAGE);  // [4 heads][HD]
+  for (int hg = 0; hg < G; hg += 4) {
+    if (hg > 0) lds_sync();
     if (n >= hg && n < min(G, hg + 4)) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.mg.o[wave][n - hg][16 * dt + 4 * g + i] = o[dt][i];
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(own + (n - hg) * HD + 16 * dt + 4 * g) = o[dt];
       if (g == 0) {
-        sm.mg.m[wave][n - hg] = mx;
-        sm.mg.l[wave][n - hg] = ls;
+        sm.u.dec.m[wave][n - hg] = mx;
+        sm.u.dec.l[wave][n - hg] = ls;
       }
     }
-    __syncthreads();
-    const int nh = min(4, G - hg);
-    for (int idx = tid; idx < nh * HD; idx += NT) {
-      const int hl = idx / HD, d = idx % HD, hn = hg + hl;
+    lds_sync();
+    const int hn = hg + wave;
+    if (hn < G) {
       float M = NEG_INF;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.mg.m[w][hl]);
-      float Ls = 0.0f, O = 0.0f;
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.u.dec.m[w][wave]);
+      float Ls = 0.0f;
+      float2 acc = make_float2(0.0f, 0.0f);
+      const int d = 2 * lane;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float mw = sm.mg.m[w][hl];
+        const float mw = sm.u.dec.m[w][wave];
         const float f = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-        Ls += f * sm.mg.l[w][hl];
-        O += f * sm.mg.o[w][hl][d];
+        Ls += f * sm.u.dec.l[w][wave];
+        const float2 v = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(st1 + w * WSTAGE) +
+                                                          wave * HD + d);
+        acc.x += f * v.x;
+        acc.y += f * v.y;
       }
       if (nch == 1) {
-        p.out[(int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d] =
-            (uint16_t)f32_to_bf16_bits(Ls > 0.0f ? O / Ls : 0.0f);
+        const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+        store4(p.out + (int64_t)md.b * p.out_stride + (int64_t)(md.h * G + hn) * HD + d,
+               pack_bf16x2(acc.x * inv, acc.y * inv));
       } else {
-        store_partial(part + hn * HD + d, O);
-        if (d == 0) {
-          store_partial(part + G * HD + 2 * hn, M);
-          store_partial(part + G * HD + 2 * hn + 1, Ls);
-        }
+        store8_agent(part + hn * HD + d, u32x2{__float_as_uint(acc.x), __float_as_uint(acc.y)});
+        if (lane == 0) store8_agent(part + G * HD + 4 * hn, u32x2{__float_as_uint(M), __float_as_uint(Ls)});
       }
     }
   }
-  if (nch == 1) return;
+  lds_sync();
+}
 
-  // Split-K: the last chunk of (row, kv head) to finish merges all partials.
-  __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged at the coherence point
-  __syncthreads();
-  if (tid == 0) {
-    const int ticket = atomicAdd(&p.counters[b * p.hkv + h], 1);
-    sm.last = ticket == nch - 1;
-  }
-  __syncthreads();
-  if (!sm.last) return;
-  const int first = dindex - (c * p.hkv + h);
-  const size_t pstride = (size_t)p.hkv * G * (HD + 2);  // floats between chunks of one (row, head)
-  const float* p0 = p.partials + (size_t)(first + h) * G * (HD + 2);
-  for (int idx = tid; idx < G * HD; idx += NT) {
-    const int hn = idx / HD, d = idx % HD;
-    // One online pass over the chunks; 8 chunks' loads are in flight at a time.
-    float M = NEG_INF, Ls = 0.0f, O = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 8) {
-      float mc[8], lc[8], oc[8];
+// Final split-K merge of (row b, kv head h): a thread owns one query head and
+// two adjacent d; the chunks' (m, l) and accumulator pairs are read 16 chunks
+// at a time (agent-scope 8-byte loads), merged online, and the ticket reset.
+__device__ __forceinline__ float2 load_partial2(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(float2, v);
+}
+
+__device__ __forceinline__ void decode_final(const Params& p, int b, int h, int dfirst, int nch, int tid) {
+  const int G = p.G;
+  const size_t pstride = (size_t)p.hkv * G * PREC;  // floats between chunks of one (row, head)
+  const float* p0 = p.partials + (size_t)dfirst * G * PREC;
+  for (int u = tid; u < G * (HD / 2); u += NT) {
+    const int hn = u / (HD / 2), d = 2 * (u % (HD / 2));
+    float M = NEG_INF, Ls = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      float2 ml[16], ov[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const bool ok = c0 + u < nch;
-        const float* pc = p0 + (size_t)(ok ? c0 + u : c0) * pstride;
-        mc[u] = ok ? load_partial(pc + G * HD + 2 * hn) : NEG_INF;
-        lc[u] = ok ? load_partial(pc + G * HD + 2 * hn + 1) : 0.0f;
-        oc[u] = ok ? load_partial(pc + hn * HD + d) : 0.0f;
+      for (int k = 0; k < 16; ++k) {
+        const bool ok = c0 + k < nch;
+        const float* pc = p0 + (size_t)(ok ? c0 + k : c0) * pstride;
+        ml[k] = ok ? load_partial2(pc + G * HD + 4 * hn) : make_float2(NEG_INF, 0.0f);
+        ov[k] = ok ? load_partial2(pc + hn * HD + d) : make_float2(0.0f, 0.0f);
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float mn = fmaxf(M, mc[u]);
+      for (int k = 0; k < 16; ++k) {
+        const float mn = fmaxf(M, ml[k].x);
         if (mn == NEG_INF) continue;
-        const float a = __builtin_amdgcn_exp2f(M - mn), bw = __builtin_amdgcn_exp2f(mc[u] - mn);
-        Ls = Ls * a + lc[u] * bw;
-        O = O * a + oc[u] * bw;
+        const float a = __builtin_amdgcn_exp2f(M - mn), bw = __builtin_amdgcn_exp2f(ml[k].x - mn);
+        Ls = Ls * a + ml[k].y * bw;
+        O0 = O0 * a + ov[k].x * bw;
+        O1 = O1 * a + ov[k].y * bw;
         M = mn;
       }
     }
-    p.out[(int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d] =
-        (uint16_t)f32_to_bf16_bits(Ls > 0.0f ? O / Ls : 0.0f);
+    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    *reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d) =
+        pack_bf16x2(O0 * inv, O1 * inv);
   }
   if (tid == 0) atomicExch(&p.counters[b * p.hkv + h], 0);
 }
 
+// Split-K merge tasks, one per (decode row, kv head) in row-major order, are
+// spread over the work lists (task t on list t % nlist) and taken from each
+// list's own counter by that list's workgroups once their items are done.  A
+// task waits until all chunk tickets of its (row, head) have arrived (each
+// chunk increments the ticket only after its partial stores are complete, and
+// the chunks are processed by running workgroups that never wait on merge
+// tasks), merges, and resets the ticket for the next launch.  Like the work
+// lists, a counter only grows: a launch makes exactly tasks + workgroups
+// fetches on it, and the workgroup making the last one advances its base.
+__device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int tid) {
+  uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (NLIST + list) * CTRL_STRIDE;
+  const int ntask = p.nd * p.hkv;
+  const uint32_t count = list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u;
+  const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
+  if (tid == 0) sm.base = __hip_atomic_load(mctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  lds_sync();
+  const uint32_t base = sm.base;
+  for (;;) {
+    if (tid == 0) sm.item = atomicAdd(mctr, 1u) - base;
+    lds_sync();
+    const uint32_t rel = __builtin_amdgcn_readfirstlane(sm.item);
+    lds_sync();
+    if (rel >= count) {
+      if (tid == 0 && rel == count + wgs - 1u)
+        __hip_atomic_store(mctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    const int task = list + (int)rel * nlist;
+    const int b = task / p.hkv, h = task % p.hkv;
+    const int L = min(max(p.dlens[b], 0), p.dtab_width * p.block_size);
+    const int nch = max(1, (L + CHUNK - 1) / CHUNK);
+    if (nch == 1) continue;
+    int* ticket = &p.counters[b * p.hkv + h];
+    if (tid == 0)
+      while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nch) __builtin_amdgcn_s_sleep(2);
+    lds_sync();
+    decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, nch, tid);
+  }
+}
+
+// Runs this workgroup's remaining items, all decode items, starting with
+// relative index rel0 (row r0), and returns with sm.item holding the last
+// (out-of-list) fetch result.  Every fetch issued is consumed, and none is
+// issued after an out-of-list one.
+template <bool FP8>
+__device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
+                           uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
+                           int r0, int tid) {
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  uint8_t* sa = st0 + wave * WSTAGE;  // step 0 of every item
+  uint8_t* sb = st1 + wave * WSTAGE;  // step 1
+  constexpr int GROUP = d_group<FP8>();
+
+  uint32_t f = 0;
+  if (tid == 0) f = atomic_add_ret(ctr, 1u);  // issued before the loads, so its wait drains nothing
+  DMeta cur = decode_meta(p, sm, list + (int)rel0 * nlist, r0, decode_base);
+  decode_issue_q(p, qbuf, cur, wave, lane);
+  decode_issue<FP8>(p, sa, cur, 0, wave, lane);
+  decode_issue<FP8>(p, sb, cur, 1, wave, lane);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 + 2 * GROUP));  // the fetch (and nothing issued after it)
+  if (tid == 0) sm.item = after_wait(f) - base;
+  lds_sync();
+  uint32_t rel = __builtin_amdgcn_readfirstlane(sm.item);
+  bool has_next = rel < count;
+  DMeta nxt = cur;
+  if (has_next) {
+    const int item = list + (int)rel * nlist;
+    nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
+  }
+
+  DMeta prev = cur;         // item whose partial was stored last
+  bool ticket_due = false;  // prev's partial is stored and its ticket not yet taken
+  for (;;) {
+    // Step 0: Q and step 0 landed; only step 1 (GROUP loads) may be in flight.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
+    lds_sync();  // every wavefront's quarter of Q has landed
+    u32x4 qv[4];
+    {
+      const int hn = min(n, p.G - 1);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qbuf + hn * ROWB + 16 * (4 * kk + g));
+    }
+    // Every wavefront's partial stores of the previous item are complete (each
+    // waited past them, then the barrier): its ticket goes out.  The next
+    // fetch goes out here too; its result is read after step 1's wait.
+    if (tid == 0 && ticket_due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
+    ticket_due = false;
+    if (tid == 0 && has_next) f = atomic_add_ret(ctr, 1u);
+
+    f32x4 o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
+    float m = NEG_INF, l = 0.0f;
+    decode_step<FP8>(p, sa, decode_ntok(p, cur, 0, wave), qv, o, m, l, lane);
+    decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
+
+    // Step 1: only the next item's step 0 may be in flight.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
+    decode_step<FP8>(p, sb, decode_ntok(p, cur, 1, wave), qv, o, m, l, lane);
+
+    lds_sync();  // every wavefront is done with Q and the merge area
+    decode_issue_q(p, qbuf, nxt, wave, lane);
+    // The fetch was issued before the loads step 1 waited past.
+    if (tid == 0 && has_next) sm.item = after_wait(f) - base;
+    decode_merge(p, sm, st1, cur, tid, o, m, l);
+    decode_issue<FP8>(p, sb, nxt, 1, wave, lane);
+    prev = cur;
+    ticket_due = decode_nch(p, cur) > 1;
+    if (!has_next) break;
+    cur = nxt;
+    rel = __builtin_amdgcn_readfirstlane(sm.item);
+    has_next = rel < count;
+    if (has_next) {
+      const int item = list + (int)rel * nlist;
+      nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
+    }
+  }
+  // The last item's partial stores (and the repeated loads) complete here.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  lds_sync();
+  if (tid == 0 && ticket_due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
+}
+
 // --------------------------------------------------------------- prefill item
 template <bool FP8>
-__device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int tid) {
+__device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int hg = local % p.HG;
@@ -601,7 +860,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
   const int npages = paged ? (kend + p.block_size - 1) / p.block_size : 0;
   const bool cached = npages <= MAX_PAGES;
   typedef __attribute__((address_space(3))) const int lds_int;
-  lds_int* pages = (lds_int*)(sm.pages);
+  lds_int* pages = (lds_int*)(sm.u.pf.pages);
   // Lane-constant element offsets of this thread's 4 tile rows (row
   // (tid>>4)+16*it, swizzled 16-byte chunk) from the tile's first key.
   const int krow = paged ? p.hkv * HD : (int)p.k_stride;  // row strides < 2^25 elements (checked on the host)
@@ -652,8 +911,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
     if (nv == TT) {  // full tile: DMA only
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], (buf ? st1 : st0) + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], (buf ? st1 : st0) + TILE_BYTES + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
       }
       return;
     }
@@ -661,11 +920,11 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
       if (row < nv) {
-        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], sm.u.pf.k[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], sm.u.pf.v[buf] + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], (buf ? st1 : st0) + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], (buf ? st1 : st0) + TILE_BYTES + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
       } else {
-        st16(sm.u.pf.k[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
-        st16(sm.u.pf.v[buf] + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
+        st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
+        st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
       }
     }
   };
@@ -674,12 +933,12 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
-      st16(sm.u.pf.k[buf] + row * ROWB + ((tid & 15) << 4), kr[it]);
-      st16(sm.u.pf.v[buf] + row * ROWB + ((tid & 15) << 4), vr[it]);
+      st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), kr[it]);
+      st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), vr[it]);
     }
     if (tid < TT) {
-      sm.ks[buf][tid] = ksr;
-      sm.vs[buf][tid] = vsr;
+      sm.u.pf.ks[buf][tid] = ksr;
+      sm.u.pf.vs[buf][tid] = vsr;
     }
   };
 
@@ -693,7 +952,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
 
   // The row's block table goes to LDS once, so no tile waits on a table load.
   if (cached)
-    for (int i = tid; i < npages; i += NT) sm.pages[i] = prow[i];
+    for (int i = tid; i < npages; i += NT) sm.u.pf.pages[i] = prow[i];
   __syncthreads();
   if (kend > 0) {
     issue_tile(0, 0);
@@ -707,8 +966,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
     const bool more = kv0 + TT < kend;
     if (more) issue_tile(kv0 + TT, buf ^ 1);
     if (active) {
-      const uint8_t* kt = sm.u.pf.k[buf];
-      const uint8_t* vt = sm.u.pf.v[buf];
+      const uint8_t* kt = buf ? st1 : st0;
+      const uint8_t* vt = kt + TILE_BYTES;
 
       // S^T = K Q^T; the next K fragment is read while the current one feeds the MFMAs.
       f32x4 s[4][NQT];
@@ -731,7 +990,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
       const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
       bf16x8 pb[NQT][2];
       const int lim0 = q0 + n + prefix;
-      prefill_softmax<true>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.ks[buf], sm.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
+      prefill_softmax<true>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
 
       // O^T += V^T P^T; the next V^T operand is read while the current one feeds the MFMAs.
       auto vload = [&](int i) {
@@ -771,6 +1030,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, int r, int local, int ti
 template <bool FP8>
 __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   __shared__ Smem sm;
+  __shared__ __attribute__((aligned(16))) uint8_t stage0[STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t stage1[STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[MAX_G * HD * 2];  // decode: Q of the current item
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
@@ -849,38 +1111,19 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       const int item = list + (int)rel * nlist;
       uint32_t next = 0;
       if (tid == 0) next = atomicAdd(ctr, 1u) - base;  // fetched ahead, consumed at the end
-      prefill_item<FP8>(p, sm, r, item - sm.off[r], ltid);
+      prefill_item<FP8>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
       rel = advance(next);
       r = resolve(rel);
       continue;
     }
-    // A run of decode items: the next item's loads are issued before the
-    // current item's merge tail, so HBM stays busy across items.
-    DecodeState st;
-    {
-      const int item = list + (int)rel * nlist;
-      decode_issue<FP8>(p, sm, st, r - p.np, item - sm.off[r], item - decode_base, ltid);
-    }
-    for (;;) {
-      uint32_t next = 0;
-      if (tid == 0) next = atomicAdd(ctr, 1u) - base;
-      f32x4 o[8];
-      float mx, ls;
-      decode_compute<FP8>(p, sm, st, ltid, o, mx, ls);
-      const int cb = st.b, chd = st.h, cc = st.c, cn = st.nch, cdi = st.dindex;
-      rel = advance(next);
-      r = resolve(rel);
-      const bool more = r >= p.np;
-      if (more) {
-        const int item = list + (int)rel * nlist;
-        decode_issue<FP8>(p, sm, st, r - p.np, item - sm.off[r], item - decode_base, ltid);
-      }
-      decode_tail(p, sm, cb, chd, cc, cn, cdi, ltid, o, mx, ls);
-      if (!more) break;
-    }
+    // Decode items come after every prefill item of the list, so the rest of
+    // this workgroup's list is one streaming decode run.
+    decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, ltid);
+    break;
   }
   if (tid == 0 && sm.item == count + wgs - 1u)
     __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (p.nd > 0) merge_tasks(p, sm, list, nlist, decode_base, tid);
 }
 
 struct DeviceShape {
@@ -913,7 +1156,7 @@ int device_shape(DeviceShape* out) {
   return SLO_OK;
 }
 
-size_t partial_floats(int64_t items, int G) { return (size_t)items * G * (HD + 2); }
+size_t partial_floats(int64_t items, int G) { return (size_t)items * G * PREC; }
 
 }  // namespace slo
 
