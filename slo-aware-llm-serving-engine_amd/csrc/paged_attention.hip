@@ -62,15 +62,15 @@ constexpr int TT = 64;                 // tokens per tile
 constexpr int CHUNK = 128;             // decode split-K chunk (tokens)
 constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
 constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
-constexpr int NQT = 2;                 // 16-position column tiles per prefill wavefront
-constexpr int BQ = 16 * NQT;           // query positions per prefill item
+constexpr int BQ_MIN = 16;             // query positions per prefill item: 16 or 32 (per launch)
 constexpr int MAX_ROWS = 1024;         // decode + prefill rows per launch
 constexpr int MAX_G = 16;              // query heads per kv head
 constexpr int MAX_PAGES = 256;         // prefill block-table entries cached in LDS
 constexpr int NLIST = 8;          // work lists (one per XCD)
 constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
-// Control words: one line per work list, then one per split-K merge-task list.
-constexpr int CTRL_BYTES = 2 * NLIST * CTRL_STRIDE * 4;
+// Control words: one line per prefill work list, per decode work list and per
+// split-K merge-task list.
+constexpr int CTRL_BYTES = 3 * NLIST * CTRL_STRIDE * 4;
 constexpr int MAX_COUNTERS = 65536;
 constexpr int PREC = HD + 4;      // floats per query head in a split-K partial: acc[HD], m, l, 2 pad
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
@@ -135,6 +135,7 @@ struct Smem {
   } u;
   int off[MAX_ROWS + 1];
   int wsum[4];
+  int wmax[4];
   uint32_t item;
   uint32_t base;
   int row;
@@ -204,7 +205,7 @@ __device__ __forceinline__ float col_sum(float x) {
 // positive factor c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA
 // and one v_exp_f32 per score.  MASK selects the boundary-tile path (keys past
 // the tile's valid rows or causally after the column).
-template <bool MASK>
+template <bool MASK, int NQT>
 __device__ __forceinline__ void prefill_softmax(f32x4 (&s)[4][NQT], float (&m)[NQT], float (&l)[NQT],
                                                 f32x4 (&o)[8][NQT], bf16x8 (&pb)[NQT][2], float c, bool src_fp8,
                                                 const float* ks, const float* vs, int g, int ntok, int kv0,
@@ -261,10 +262,42 @@ __device__ __forceinline__ int decode_len(const Params& p, int b) {
   return min(max(L, 0), p.dtab_width * p.block_size);
 }
 
-__device__ __forceinline__ int row_items(const Params& p, int r) {
+// Prefill row geometry: query range, usable keys and the bottom-right causal
+// offset (keys before the first query position).
+struct PfRow {
+  int q_start, Lq, k_start, Lk, prefix;
+};
+__device__ __forceinline__ PfRow pf_row(const Params& p, int r) {
+  PfRow g;
+  g.q_start = p.cu_q[r];
+  g.Lq = p.cu_q[r + 1] - g.q_start;
+  g.k_start = p.cu_k[r];
+  const int lk_full = p.cu_k[r + 1] - g.k_start;
+  g.prefix = lk_full - g.Lq;
+  int lk = lk_full;
+  if (p.ptab != nullptr) lk = min(lk, p.ptab_width * p.block_size);
+  else lk = min(lk, p.num_kv_rows - g.k_start);
+  g.Lk = max(lk, 0);
+  return g;
+}
+
+// Key tiles of the heaviest 32-position block of a prefill row, and an
+// estimate of the row's total tile work (blocks x mean tiles x kv heads x
+// head groups).
+__device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& tmax) {
+  const PfRow g = pf_row(p, r);
+  work = tmax = 0;
+  if (g.Lq <= 0) return;
+  const int nqb = (g.Lq + 31) / 32;
+  tmax = (min(g.Lk, max(0, g.prefix + g.Lq)) + TT - 1) / TT;
+  const int mean = (min(g.Lk, max(0, g.prefix + (g.Lq + 1) / 2)) + TT - 1) / TT;
+  work = nqb * max(mean, 1) * p.hkv * p.HG;
+}
+
+__device__ __forceinline__ int row_items(const Params& p, int r, int bq) {
   if (r < p.np) {
     const int lq = p.cu_q[r + 1] - p.cu_q[r];
-    return lq > 0 ? ((lq + BQ - 1) / BQ) * p.hkv * p.HG : 0;
+    return lq > 0 ? ((lq + bq - 1) / bq) * p.hkv * p.HG : 0;
   }
   const int L = decode_len(p, r - p.np);
   return max(1, (L + CHUNK - 1) / CHUNK) * p.hkv;
@@ -682,7 +715,7 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // lists, a counter only grows: a launch makes exactly tasks + workgroups
 // fetches on it, and the workgroup making the last one advances its base.
 __device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int tid) {
-  uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (NLIST + list) * CTRL_STRIDE;
+  uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (2 * NLIST + list) * CTRL_STRIDE;
   const int ntask = p.nd * p.hkv;
   const uint32_t count = list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u;
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
@@ -728,7 +761,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 
   uint32_t f = 0;
   if (tid == 0) f = atomic_add_ret(ctr, 1u);  // issued before the loads, so its wait drains nothing
-  DMeta cur = decode_meta(p, sm, list + (int)rel0 * nlist, r0, decode_base);
+  DMeta cur = decode_meta(p, sm, decode_base + list + (int)rel0 * nlist, r0, decode_base);
   decode_issue_q(p, qbuf, cur, wave, lane);
   decode_issue<FP8>(p, sa, cur, 0, wave, lane);
   decode_issue<FP8>(p, sb, cur, 1, wave, lane);
@@ -739,7 +772,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   bool has_next = rel < count;
   DMeta nxt = cur;
   if (has_next) {
-    const int item = list + (int)rel * nlist;
+    const int item = decode_base + list + (int)rel * nlist;
     nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
   }
 
@@ -786,7 +819,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     rel = __builtin_amdgcn_readfirstlane(sm.item);
     has_next = rel < count;
     if (has_next) {
-      const int item = list + (int)rel * nlist;
+      const int item = decode_base + list + (int)rel * nlist;
       nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
     }
   }
@@ -797,8 +830,9 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // --------------------------------------------------------------- prefill item
-template <bool FP8>
+template <bool FP8, int NQT>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
+  constexpr int BQ = 16 * NQT;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int hg = local % p.HG;
@@ -806,16 +840,10 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   const int h = t % p.hkv;
   const int qb_rev = t / p.hkv;
 
-  const int q_start = p.cu_q[r];
-  const int Lq = p.cu_q[r + 1] - q_start;
-  const int k_start = p.cu_k[r];
-  const int Lk_full = p.cu_k[r + 1] - k_start;
-  const int prefix = Lk_full - Lq;  // bottom-right causal alignment
+  const PfRow geo = pf_row(p, r);
+  const int q_start = geo.q_start, Lq = geo.Lq, k_start = geo.k_start, Lk = geo.Lk;
+  const int prefix = geo.prefix;  // bottom-right causal alignment
   const bool paged = p.ptab != nullptr;
-  int Lk = Lk_full;
-  if (paged) Lk = min(Lk, p.ptab_width * p.block_size);
-  else Lk = min(Lk, p.num_kv_rows - k_start);
-  Lk = max(Lk, 0);
 
   const int nqb = (Lq + BQ - 1) / BQ;
   const int q0 = (nqb - 1 - qb_rev) * BQ;  // heaviest blocks are pulled first
@@ -990,7 +1018,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
       bf16x8 pb[NQT][2];
       const int lim0 = q0 + n + prefix;
-      prefill_softmax<true>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
+      prefill_softmax<true, NQT>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
 
       // O^T += V^T P^T; the next V^T operand is read while the current one feeds the MFMAs.
       auto vload = [&](int i) {
@@ -1036,11 +1064,45 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
-  // Per-row item counts -> exclusive prefix in sm.off (block-wide scan).
   const int per = (nrows + NT - 1) / NT;
   const int r0 = tid * per;
+
+  // Prefill block size: 16 query positions when the heaviest 32-position
+  // block would take more than twice a workgroup's fair share of the prefill
+  // work (the launch would wait on that one item), else 32.
+  int bq = 32;
+  if (p.np > 0) {
+    int w = 0, tm = 0;
+    for (int r = r0; r < min(r0 + per, p.np); ++r) {
+      int wr, tr;
+      pf_work(p, r, wr, tr);
+      w += wr;
+      tm = max(tm, tr);
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      w += __shfl_xor(w, d, 64);
+      tm = max(tm, __shfl_xor(tm, d, 64));
+    }
+    if (lane == 0) {
+      sm.wsum[wave] = w;
+      sm.wmax[wave] = tm;
+    }
+    __syncthreads();
+    int64_t wt = 0;
+    int tmax = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wt += sm.wsum[i];
+      tmax = max(tmax, sm.wmax[i]);
+    }
+    if ((int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
+    __syncthreads();
+  }
+
+  // Per-row item counts -> exclusive prefix in sm.off (block-wide scan).
   int local_sum = 0;
-  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r);
+  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r, bq);
   int incl = local_sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -1053,76 +1115,93 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   for (int w = 0; w < wave; ++w) run += sm.wsum[w];
   for (int r = r0; r < min(r0 + per, nrows); ++r) {
     sm.off[r] = run;
-    run += row_items(p, r);
+    run += row_items(p, r, bq);
   }
   if (tid == NT - 1) sm.off[nrows] = run;
   __syncthreads();
   const int total = sm.off[nrows];
   const int decode_base = sm.off[p.np];
 
-  // Work lists: item i belongs to list i % nlist and workgroup b serves list
-  // b % nlist, so the lists' fetch counters are separate addresses (and, with
-  // round-robin dispatch and 8 kv heads, one kv head's prefill tiles stay on
-  // one XCD's L2).  A list's counter only grows; the list's base is the
-  // counter value at which this launch's items start.  Every workgroup reads
-  // the base before its first fetch and stops after its first fetch past the
-  // list, so a launch makes exactly count + workgroups fetches on a list and
-  // the workgroup that makes the last one advances the base for the next
-  // launch.  No counter is ever reset or contended by a completion count.
+  // Work lists.  Prefill items [0, decode_base) and decode items
+  // [decode_base, total) form two families; item i of a family belongs to list
+  // i % nlist of that family and workgroup b serves list b % nlist of both, so
+  // the lists' fetch counters are separate addresses (and, with round-robin
+  // dispatch and 8 kv heads, one kv head's prefill tiles stay on one XCD's
+  // L2).  Alternate workgroups of a list start with different families and
+  // take the other one when theirs is exhausted, so MFMA-bound prefill items
+  // and HBM-bound decode items run side by side from the start.  A list's
+  // counter only grows; the list's base is the counter value at which this
+  // launch's items start.  Every workgroup reads the base before its first
+  // fetch and stops after its first fetch past the list, so a launch makes
+  // exactly count + workgroups fetches on a list and the workgroup that makes
+  // the last one advances the base for the next launch.  No counter is ever
+  // reset or contended by a completion count.
   const int nlist = min((int)gridDim.x, NLIST);
   const int list = blockIdx.x % nlist;
-  const uint32_t count = list < total ? (uint32_t)((total - list + nlist - 1) / nlist) : 0u;
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
-  uint32_t* ctr = reinterpret_cast<uint32_t*>(p.ctrl) + list * CTRL_STRIDE;
-  if (tid == 0) {
-    sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm.salt = 0;
-    sm.item = atomicAdd(ctr, 1u) - sm.base;  // relative fetch index
-  }
-  __syncthreads();
-  const uint32_t base = sm.base;
-
-  // Publishes the fetched-ahead index to the workgroup and returns it.
-  auto advance = [&](uint32_t next) -> uint32_t {
-    __syncthreads();
-    if (tid == 0) sm.item = next;
-    __syncthreads();
-    return sm.item;
-  };
-  // Row of relative index `rel`, or -1 past the end of the list.
-  auto resolve = [&](uint32_t rel) -> int {
-    if (rel >= count) return -1;
-    const int item = list + (int)rel * nlist;
-    for (int r = tid; r < nrows; r += NT)
-      if (sm.off[r] <= item && item < sm.off[r + 1]) sm.row = r;
-    __syncthreads();
-    return sm.row;
-  };
-
-  uint32_t rel = sm.item;
-  __syncthreads();
-  int r = resolve(rel);
-  while (r >= 0) {
-    // sm.salt is always 0; reading it here keeps the lane-derived values of the
-    // two item paths from being hoisted out of the loop, where they would all
-    // stay live at once.
-    const int ltid = tid + sm.salt;
-    if (r < p.np) {
-      const int item = list + (int)rel * nlist;
-      uint32_t next = 0;
-      if (tid == 0) next = atomicAdd(ctr, 1u) - base;  // fetched ahead, consumed at the end
-      prefill_item<FP8>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-      rel = advance(next);
-      r = resolve(rel);
-      continue;
+  const int first = (blockIdx.x / nlist) & 1;  // family taken first: 0 prefill, 1 decode
+  if (tid == 0) sm.salt = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int fam = first ^ pass;
+    const int fbase = fam ? decode_base : 0;
+    const int fsize = fam ? total - decode_base : decode_base;
+    const uint32_t count = list < fsize ? (uint32_t)((fsize - list + nlist - 1) / nlist) : 0u;
+    // A list without items this launch is not touched: its base stays valid.
+    if (count == 0) continue;
+    uint32_t* ctr = reinterpret_cast<uint32_t*>(p.ctrl) + (fam * NLIST + list) * CTRL_STRIDE;
+    if (tid == 0) {
+      sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm.item = atomicAdd(ctr, 1u) - sm.base;  // relative fetch index
     }
-    // Decode items come after every prefill item of the list, so the rest of
-    // this workgroup's list is one streaming decode run.
-    decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, ltid);
-    break;
+    __syncthreads();
+    const uint32_t base = sm.base;
+
+    // Publishes the fetched-ahead index to the workgroup and returns it.
+    auto advance = [&](uint32_t next) -> uint32_t {
+      __syncthreads();
+      if (tid == 0) sm.item = next;
+      __syncthreads();
+      return sm.item;
+    };
+    // Row of relative index `rel`, or -1 past the end of the list.
+    auto resolve = [&](uint32_t rel) -> int {
+      if (rel >= count) return -1;
+      const int item = fbase + list + (int)rel * nlist;
+      for (int r = tid; r < nrows; r += NT)
+        if (sm.off[r] <= item && item < sm.off[r + 1]) sm.row = r;
+      __syncthreads();
+      return sm.row;
+    };
+
+    uint32_t rel = sm.item;
+    __syncthreads();
+    int r = resolve(rel);
+    while (r >= 0) {
+      // sm.salt is always 0; reading it here keeps the lane-derived values of
+      // the two item paths from being hoisted out of the loop, where they
+      // would all stay live at once.
+      const int ltid = tid + sm.salt;
+      if (r < p.np) {
+        const int item = list + (int)rel * nlist;
+        if (bq == 16) prefill_item<FP8, 1>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+        else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+        // The next item is fetched only now: fetching ahead would let a
+        // workgroup claim a second item before a late-starting one takes its
+        // first.
+        uint32_t next = 0;
+        if (tid == 0) next = atomicAdd(ctr, 1u) - base;
+        rel = advance(next);
+        r = resolve(rel);
+        continue;
+      }
+      // The rest of this decode list is one streaming decode run.
+      decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, ltid);
+      break;
+    }
+    if (tid == 0 && sm.item == count + wgs - 1u)
+      __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
   }
-  if (tid == 0 && sm.item == count + wgs - 1u)
-    __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (p.nd > 0) merge_tasks(p, sm, list, nlist, decode_base, tid);
 }
 
@@ -1275,7 +1354,7 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   if (do_dec) bound += (int64_t)p.nd * ((dec_len_cap + CHUNK - 1) / CHUNK) * p.hkv;
   if (do_pf) {
     const int64_t tq = std::max<int64_t>(0, a->num_q_rows - a->num_decode);
-    bound += (tq / BQ + p.np) * p.hkv * p.HG;
+    bound += (tq / BQ_MIN + p.np) * p.hkv * p.HG;
   }
   const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8 ? 1 : 0];
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));

@@ -41,7 +41,7 @@ def test_workspace_bytes_and_errors():
     # one record of G x (128 accumulators + m + l + 2 pad) floats per 128-token chunk
     per_item = 4 * (128 + 4) * 4
     assert n2 - n1 == 24 * (4096 // 128) * 8 * per_item
-    assert n0 == 16 * 128 + 4 * 65536
+    assert n0 == 24 * 128 + 4 * 65536
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.workspace_bytes(1, 1, 32, 8, 64)
     with pytest.raises(RuntimeError):
