@@ -6,15 +6,20 @@
 //
 // Work list.  Every workgroup (4 wavefronts, two workgroups per CU) first
 // derives, from the metadata alone, the number of work items of every row and
-// their exclusive prefix (prefill rows first, then decode rows), then pulls
-// item indices from a device counter (one fetch ahead) until the list is
-// exhausted.  The grid is sized from capacities, never from device data, so
-// the launch can be recorded in a HIP graph.  The counter and the split-K
-// tickets reset themselves at the end of every launch, so no memset is needed.
+// their exclusive prefix (prefill rows first, then decode rows).  Item i
+// belongs to list i % 8 and workgroup b serves list b % 8; the prefill items
+// and the decode items of a list form two families, and workgroups start with
+// one family or the other alternately so both phases begin at once.  Each list
+// has a monotonic fetch counter and a base word on its own 128-byte line: the
+// workgroup that makes a family's last fetch advances its base, so counters
+// never need a reset or memset.  The grid is sized from capacities, never from
+// device data, so the launch can be recorded in a HIP graph.
 //
-//  * Prefill item (row r, block of 32 query positions, kv head h): each
+//  * Prefill item (row r, block of 16 or 32 query positions, kv head h): each
 //    wavefront owns one of the G query heads that share kv head h, for the
-//    same positions, so the K/V tiles staged in LDS serve all G heads.  Tiles
+//    same positions, so the K/V tiles staged in LDS serve all G heads.  The
+//    block size is chosen per launch: 16 when the heaviest row's items would
+//    otherwise outlast the balanced share of a workgroup, else 32.  Tiles
 //    of 64 keys are double-buffered: the next tile's global loads are in
 //    flight while the current one is consumed.  The contraction runs on bf16
 //    MFMA (v_mfma_f32_16x16x32_bf16) in the transposed form S^T = K Q^T,
