@@ -208,32 +208,51 @@ __device__ __forceinline__ float col_sum(float x) {
 // Online-softmax update of one prefill tile for the wavefront's NQT query
 // columns.  Scores stay unscaled until the exponent: max commutes with the
 // positive factor c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA
-// and one v_exp_f32 per score.  MASK selects the boundary-tile path (keys past
-// the tile's valid rows or causally after the column).
-template <bool MASK, int NQT>
+// and one v_exp_f32 per score.  `mask` selects the boundary-tile path (keys
+// past the tile's valid rows or causally after the column).
+// The running max used as the exponent offset moves only when a tile's max
+// exceeds it by more than 2^RESCALE_LOG2 (in units of the log2-scaled score),
+// so every probability stays <= 2^RESCALE_LOG2 (exact in bf16's range, far
+// from fp32 overflow in the row sum) and O is rescaled only on those rare
+// tiles.  The result o / l is the same quantity as with an exact running max.
+constexpr float RESCALE_LOG2 = 8.0f;
+
+template <int NQT>
 __device__ __forceinline__ void prefill_softmax(f32x4 (&s)[4][NQT], float (&m)[NQT], float (&l)[NQT],
                                                 f32x4 (&o)[8][NQT], bf16x8 (&pb)[NQT][2], float c, bool src_fp8,
-                                                const float* ks, const float* vs, int g, int ntok, int kv0,
+                                                const float* ks, const float* vs, int g, bool mask, int ntok, int kv0,
                                                 int lim0) {
 #pragma unroll
   for (int nt = 0; nt < NQT; ++nt) {
-    const int lim = lim0 + 16 * nt;  // last visible key index of this column
+    if (src_fp8) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[mt][nt][i] *= ks[16 * mt + 4 * g + i];
+    }
+    // Only tiles that reach past the valid keys or the block's causal edge
+    // are masked (a wave-uniform branch).
+    if (mask) {
+      const int lim = lim0 + 16 * nt;  // last visible key index of this column
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = 16 * mt + 4 * g + i;
+          s[mt][nt][i] = (tok < ntok && kv0 + tok <= lim) ? s[mt][nt][i] : NEG_INF;
+        }
+    }
     float mx = NEG_INF;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * mt + 4 * g + i;
-        float x = s[mt][nt][i];
-        if (src_fp8) x *= ks[tok];
-        if constexpr (MASK) x = (tok < ntok && kv0 + tok <= lim) ? x : NEG_INF;
-        s[mt][nt][i] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
     mx = col_max(mx);
-    const float mnew = fmaxf(m[nt], mx);
+    // grow is false when both maxima are -inf (NaN compares false).
+    const bool grow = c * (mx - m[nt]) > RESCALE_LOG2;
+    const float mnew = grow ? mx : m[nt];
     const float cm = mnew == NEG_INF ? 0.0f : c * mnew;
-    const float alpha = __builtin_amdgcn_exp2f(c * m[nt] - cm);
+    const float alpha = grow ? __builtin_amdgcn_exp2f(c * m[nt] - cm) : 1.0f;
     float rs = 0.0f;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -246,7 +265,7 @@ __device__ __forceinline__ void prefill_softmax(f32x4 (&s)[4][NQT], float (&m)[N
     rs = col_sum(rs);
     l[nt] = l[nt] * alpha + rs;
     m[nt] = mnew;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // no column's max moved: skip the rescale
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // no column's offset moved: skip the rescale
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
     }
@@ -835,6 +854,10 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // --------------------------------------------------------------- prefill item
+#ifndef SLO_KB2
+#define SLO_KB2 8
+#endif
+constexpr int KB2 = SLO_KB2;  // LDS operand batch with two query blocks per wavefront
 template <bool FP8, int NQT>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
   constexpr int BQ = 16 * NQT;
@@ -941,11 +964,16 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
     const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
     const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
+    // Inline-asm DMA: the compiler does not track these loads, so it inserts
+    // no wait for them before the current tile's LDS reads (it cannot tell
+    // which buffer a DMA writes); the loop waits for them explicitly.
+    const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
+    const uint32_t vdst = kdst + TILE_BYTES;
     if (nv == TT) {  // full tile: DMA only
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], (buf ? st1 : st0) + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], (buf ? st1 : st0) + TILE_BYTES + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
+        dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
       }
       return;
     }
@@ -953,8 +981,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
       if (row < nv) {
-        __builtin_amdgcn_global_load_lds(ksrc + kgo[it], (buf ? st1 : st0) + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vsrc + vgo[it], (buf ? st1 : st0) + TILE_BYTES + (16 * it + 4 * wave) * ROWB, 16, 0, 0);
+        dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
+        dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
       } else {
         st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
         st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
@@ -994,28 +1022,57 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   for (int kv0 = 0, j = 0; kv0 < kend; kv0 += TT, ++j) {
     const int buf = j & 1;
     const int ntok = min(TT, kend - kv0);
-    __builtin_amdgcn_s_waitcnt(0);  // this tile's loads have landed in LDS
-    __syncthreads();                // ... for every wavefront; the other buffer is free
+    // This tile's DMA (the only one in flight) and register loads have
+    // landed; after the barrier every wavefront's part is visible and the
+    // other buffer is free.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    lds_sync();
     const bool more = kv0 + TT < kend;
+    const uint8_t* kt = buf ? st1 : st0;
+    const uint8_t* vt = kt + TILE_BYTES;
+    // The tile's MFMA operands are read from LDS in batches (all 16 K or V^T
+    // fragments with one query block, KB2 with two, where registers are
+    // short) so that one LDS round trip serves a batch, not a single MFMA.
+    // Fragment i of a batch is K rows 16*(i & 3) + n, k-step i >> 2.  With
+    // one query block the first V^T batch is read before the softmax.
+    constexpr int KB = NQT == 1 ? 16 : KB2;
+    constexpr bool VPRE = NQT == 1;
+    auto kread = [&](int i) { return ld16(kt + (i & 3) * 16 * ROWB + koff[i >> 2]); };
+    auto vread = [&](int i) {  // V^T operand: k-step i >> 3, d-tile i & 7
+      const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
+      return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
+    };
+    u32x4 kf[KB];
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < KB; ++i) kf[i] = kread(i);
+    }
+    // The next tile's loads are issued while these reads are in flight.
     if (more) issue_tile(kv0 + TT, buf ^ 1);
     if (active) {
-      const uint8_t* kt = buf ? st1 : st0;
-      const uint8_t* vt = kt + TILE_BYTES;
-
-      // S^T = K Q^T; the next K fragment is read while the current one feeds the MFMAs.
+      // S^T = K Q^T, four independent accumulator chains per query block.
       f32x4 s[4][NQT];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = f32x4{0, 0, 0, 0};
-      u32x4 kf = ld16(kt + koff[0]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {  // i = 4*mt + st
-        const int mt = i >> 2, st = i & 3;
-        const u32x4 kn = i + 1 < 16 ? ld16(kt + ((i + 1) >> 2) * 16 * ROWB + koff[(i + 1) & 3]) : kf;
+      for (int b = 0; b < 16 / KB; ++b) {
+        if (b > 0) {
 #pragma unroll
-        for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = mfma16(as_bf16x8(kf), as_bf16x8(qv[nt][st]), s[mt][nt]);
-        kf = kn;
+          for (int i = 0; i < KB; ++i) kf[i] = kread(b * KB + i);
+        }
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          const int j = b * KB + i, mt = j & 3, st = j >> 2;
+#pragma unroll
+          for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = mfma16(as_bf16x8(kf[i]), as_bf16x8(qv[nt][st]), s[mt][nt]);
+        }
+      }
+      bf16x8 vf[KB];
+      if constexpr (VPRE) {
+#pragma unroll
+        for (int i = 0; i < KB; ++i) vf[i] = vread(i);
       }
 
       // Keys that can be masked: beyond the tile's valid rows, or causally
@@ -1023,20 +1080,21 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
       bf16x8 pb[NQT][2];
       const int lim0 = q0 + n + prefix;
-      prefill_softmax<true, NQT>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask ? ntok : TT, kv0, need_mask ? lim0 : (1 << 30));
+      prefill_softmax<NQT>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask, ntok, kv0, lim0);
 
-      // O^T += V^T P^T; the next V^T operand is read while the current one feeds the MFMAs.
-      auto vload = [&](int i) {
-        const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
-        return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
-      };
-      bf16x8 va = vload(0);
+      // O^T += V^T P^T.
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const bf16x8 vn = i + 1 < 16 ? vload(i + 1) : va;
+      for (int b = 0; b < 16 / KB; ++b) {
+        if (b > 0 || !VPRE) {
 #pragma unroll
-        for (int nt = 0; nt < NQT; ++nt) o[i & 7][nt] = mfma16(va, pb[nt][i >> 3], o[i & 7][nt]);
-        va = vn;
+          for (int i = 0; i < KB; ++i) vf[i] = vread(b * KB + i);
+        }
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          const int j = b * KB + i;
+#pragma unroll
+          for (int nt = 0; nt < NQT; ++nt) o[j & 7][nt] = mfma16(vf[i], pb[nt][j >> 3], o[j & 7][nt]);
+        }
       }
     }
     if (more) commit_tile(buf ^ 1);
