@@ -64,7 +64,7 @@ namespace slo {
 constexpr int HD = 128;                // head_dim this kernel implements
 constexpr int NT = 256;                // threads per workgroup (4 wavefronts)
 constexpr int TT = 64;                 // tokens per tile
-constexpr int CHUNK = 128;             // decode split-K chunk (tokens)
+constexpr int CHUNK = 256;             // decode split-K chunk (tokens): four workgroup steps
 constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
 constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
 constexpr int BQ_MIN = 16;             // query positions per prefill item: 16 or 32 (per launch)
@@ -75,9 +75,18 @@ constexpr int NLIST = 8;          // work lists (one per XCD)
 constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
 // Control words: one line per prefill work list, per decode work list and per
 // split-K merge-task list.
-constexpr int CTRL_BYTES = 3 * NLIST * CTRL_STRIDE * 4;
+// Control area: three families of NLIST list lines (prefill, decode, merge
+// tasks), then a trash line that decode wavefronts without a query head store
+// to, so every wavefront issues the same number of stores per item.
+constexpr int TRASH_OFFSET = 3 * NLIST * CTRL_STRIDE * 4;
+constexpr int TRASH_BYTES = 1024;
+constexpr int CTRL_BYTES = TRASH_OFFSET + TRASH_BYTES;
+// Word of the control area set to 1 when a split-K merge gave up waiting
+// (SPIN_LIMIT sleeps, about 0.2 s); it is never cleared by the kernel.
+constexpr int FAULT_WORD = 2 * NLIST * CTRL_STRIDE + 2;
+constexpr int SPIN_LIMIT = 1 << 22;
 constexpr int MAX_COUNTERS = 65536;
-constexpr int PREC = HD + 4;      // floats per query head in a split-K partial: acc[HD], m, l, 2 pad
+constexpr int PREC = HD + 4;      // floats per query head in a split-K record: acc[HD], m, l, 2 pad
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -145,6 +154,8 @@ struct Smem {
   uint32_t base;
   int row;
   int salt;
+  int meta[2][8];   // decode: landed row length and block-table entries, by item parity
+  int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -335,41 +346,38 @@ __device__ __forceinline__ float load_partial(const float* p) {
 }
 
 // ---------------------------------------------------------------- decode item
-// A decode item (row b, kv head h, chunk c of CHUNK tokens) is two workgroup
-// steps of DSTEP tokens; in step s wavefront w takes the DT tokens starting at
-// c*CHUNK + s*DSTEP + w*DT.  A workgroup step lies in one KV block (block_size
-// is a multiple of 64).  Step s always uses LDS stage s, and the Q of the item
-// goes to its own LDS array, so K, V and Q all go HBM -> LDS through
-// global_load_lds_dwordx4 and no streamed data is held in registers across
-// iterations.  Every wait for the streamed data is an explicit
-// `s_waitcnt vmcnt(D_GROUP)`: vector memory operations complete in issue
-// order, and when a step is consumed exactly one later group of D_GROUP loads
-// has been issued after everything it needs.  Two steps are in flight per
-// wavefront at all times, across item boundaries.
+// A decode item (row b, kv head h, chunk c of CHUNK tokens) is NSTEP = 4
+// workgroup steps of DSTEP tokens; in step s wavefront w takes the DT tokens
+// starting at c*CHUNK + s*DSTEP + w*DT.  A workgroup step lies in one KV block
+// (block_size is a multiple of 64).  Step s uses LDS stage s & 1, private to
+// each wavefront, and the item's Q goes to one half of a double-buffered LDS
+// array, so K, V and Q all go HBM -> LDS through global_load_lds_dwordx4 and
+// no streamed data is held in registers across iterations.  Two steps are in
+// flight per wavefront at all times, across item boundaries.
 //
-// Each step issues the same number of loads: lanes past the row's length read
-// valid rows of the same block (slot 0 of the pool when the block is padding)
-// and are masked afterwards; after the last item the next-item loads repeat
-// the current item's (drained before the run ends).  Split-K partials are
-// written by wavefront 0 after the cross-wavefront merge and are complete at
-// the next item's first wait, where the ticket is taken; its result (and the
-// work-list fetch issued beside it) is read after the second wait of that
-// item, so no wait ever covers loads issued for a later step.
-//
-// Inside the decode loop every vector memory operation (LDS DMA, atomics,
-// split-K and output stores) is issued through inline assembly, so the
-// compiler inserts no vector-memory waits of its own there: its bookkeeping
-// cannot follow loads that land in LDS and would drain the pipeline.  The
-// results of the two atomics are only read after an explicit wait that covers
-// them, through an empty asm that ties the value to that point.
+// Every vector memory operation of the loop (LDS DMA, atomics, split-K and
+// output stores) is issued through inline assembly at a fixed point, in the
+// same number on every pass: steps past the row's length still issue their
+// loads (all lanes of such a step read one cache line), after the last item
+// the next-item loads repeat the current item's, a ticket with nothing due
+// adds 0, a fetch after the list's end adds 0, and a wavefront without a query
+// head stores to a trash line.  Vector memory operations complete in issue
+// order, so every wait is an exact `s_waitcnt vmcnt(N)` whose N counts the
+// operations issued after the awaited ones, and no wait covers an operation
+// issued for a later step.  (The compiler's own bookkeeping cannot follow
+// loads that land in LDS and would drain the pipeline.)  Wavefront 0 alone
+// fetches work, finds the fetched item's row, loads its length and
+// block-table entries into LDS and broadcasts the row; the fetch and ticket
+// results are read after a wait that covers them, through an empty asm that
+// ties the value to that point.
 constexpr int DT = 16;                 // tokens per wavefront step
 constexpr int DSTEP = 4 * DT;          // tokens per workgroup step
+constexpr int NSTEP = CHUNK / DSTEP;   // workgroup steps per item
 constexpr int WSTAGE = 2 * DT * ROWB;  // per wavefront and stage: K rows, then V rows (bf16)
-static_assert(CHUNK == 2 * DSTEP, "a decode item is two workgroup steps");
+constexpr int QBUF = MAX_G * HD * 2;   // bytes of one half of the Q buffer
+static_assert(NSTEP == 4, "the decode loop is written for four workgroup steps per item");
 static_assert(4 * WSTAGE <= STAGE_BYTES, "decode stage must fit the tile stage");
 
-// Loads of one wavefront step: K and V (4 + 4 bf16 DMA, or 2 + 2 E4M3FN DMA
-// plus one DMA of the 32 scales).
 template <bool FP8>
 __device__ __forceinline__ constexpr int d_group() { return FP8 ? 5 : 8; }
 
@@ -404,6 +412,12 @@ __device__ __forceinline__ void atomic_add_noret(void* p, uint32_t v) {
 __device__ __forceinline__ void store16_agent(void* p, const u32x4& v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
+__device__ __forceinline__ void store16(void* p, const u32x4& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store8(void* p, const u32x2& v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
 __device__ __forceinline__ void store8_agent(void* p, const u32x2& v) {
   asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
@@ -415,11 +429,6 @@ __device__ __forceinline__ uint32_t after_wait(uint32_t x) {
   asm volatile("" : "+v"(x));
   return x;
 }
-
-// Scalar (SMEM) loads of read-only metadata at wave-uniform addresses: they are
-// counted by lgkmcnt, so they never order against the KV loads in flight.
-typedef __attribute__((address_space(4))) const int32_t const_i32;
-__device__ __forceinline__ int sload(const int32_t* base, int64_t i) { return ((const_i32*)base)[i]; }
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits
 // for every LDS DMA write still in flight (vmcnt), which would drain the KV
@@ -437,11 +446,9 @@ __device__ __forceinline__ void lds_sync() {
 struct DMeta {
   int b, h, c, dindex;  // wave-uniform
   int len;              // dlens[b] as read (clamped where used)
-  int page[2];          // KV block of workgroup step 0 and 1
+  int page[NSTEP];      // KV block of each workgroup step
 };
 
-// The SMEM results (len, page) are used only where needed, so their latency
-// stays hidden behind the item ahead of them.
 __device__ __forceinline__ int decode_L(const Params& p, const DMeta& m) {
   return min(max(m.len, 0), p.dtab_width * p.block_size);
 }
@@ -449,23 +456,36 @@ __device__ __forceinline__ int decode_nch(const Params& p, const DMeta& m) {
   return max(1, (decode_L(p, m) + CHUNK - 1) / CHUNK);
 }
 
-__device__ __forceinline__ DMeta decode_meta(const Params& p, const Smem& sm, int item, int r, int decode_base) {
+// Item geometry from its row and index within the row.
+__device__ __forceinline__ DMeta decode_geom(const Params& p, int r, int local, int item, int decode_base) {
   DMeta m;
-  r = __builtin_amdgcn_readfirstlane(r);
-  item = __builtin_amdgcn_readfirstlane(item);
   m.b = r - p.np;
-  const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
   m.h = local % p.hkv;
   m.c = local / p.hkv;
-  m.len = sload(p.dlens, m.b);
   m.dindex = item - decode_base;
-  // Block-table entries are read here, an item ahead of their use.
+  m.len = 0;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int t0 = m.c * CHUNK + s * DSTEP;
-    m.page[s] = sload(p.dtab, (int64_t)m.b * p.dtab_stride + min(t0 / p.block_size, p.dtab_width - 1));
-  }
+  for (int s = 0; s < NSTEP; ++s) m.page[s] = -1;
   return m;
+}
+// Wavefront 0: one LDS DMA of the item's row length (lane 0) and the
+// block-table entries of its steps (lanes 1..NSTEP) into sm.meta[slot].  It
+// is counted by vmcnt like the KV loads.  (Scalar loads would share lgkmcnt
+// with LDS, so the next LDS wait would stall on their latency; a load into a
+// VGPR could be copied by the compiler before it lands.)
+__device__ __forceinline__ void decode_meta_dma(const Params& p, Smem& sm, const DMeta& m, int slot, int lane) {
+  const int s = lane - 1;
+  const int32_t* src =
+      (s >= 0 && s < NSTEP)
+          ? p.dtab + (int64_t)m.b * p.dtab_stride + min((m.c * CHUNK + s * DSTEP) / p.block_size, p.dtab_width - 1)
+          : p.dlens + m.b;
+  if (lane <= NSTEP) dma4(src, lds_addr(sm.meta[slot]));
+}
+// After a wait that covers the DMA and a barrier.
+__device__ __forceinline__ void decode_meta_read(DMeta& m, const Smem& sm, int slot) {
+  m.len = __builtin_amdgcn_readfirstlane(sm.meta[slot][0]);
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) m.page[s] = __builtin_amdgcn_readfirstlane(sm.meta[slot][1 + s]);
 }
 
 // Row of item `item` among rows [lo, nrows), searched by one wavefront.
@@ -506,9 +526,12 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
   const int n = lane & 15, g = lane >> 4;
   const int ntok = decode_ntok(p, m, s, wave);
   const int t0 = m.c * CHUNK + s * DSTEP + wave * DT;
-  const int64_t slot0 = ntok > 0 ? (int64_t)m.page[s] * p.block_size + t0 % p.block_size : 0;
-  const int row = p.hkv * HD;  // elements (bf16) or bytes (E4M3FN) between tokens
-  const int64_t base = slot0 * row + (int64_t)m.h * HD;
+  // A step without valid tokens loads the pool's first line on every lane.
+  const bool live = ntok > 0;
+  const int64_t slot0 = live ? (int64_t)m.page[s] * p.block_size + t0 % p.block_size : 0;
+  const int row = live ? p.hkv * HD : 0;  // elements (bf16) or bytes (E4M3FN) between tokens
+  const int64_t base = live ? slot0 * row + (int64_t)m.h * HD : 0;
+  const int sw = live ? 1 : 0;  // keeps the swizzled chunk offsets only for live steps
   if constexpr (!FP8) {
     const uint16_t* kc = static_cast<const uint16_t*>(p.k_cache) + base;
     const uint16_t* vc = static_cast<const uint16_t*>(p.v_cache) + base;
@@ -516,12 +539,12 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(kc + r * row + 8 * (n ^ (r & 15)), dst + i * 1024);
+      dma16(kc + r * row + sw * 8 * (n ^ (r & 15)), dst + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(vc + r * row + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
+      dma16(vc + r * row + sw * 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
     }
   } else {
     const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
@@ -530,17 +553,17 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
+      dma16(kc + r * row + sw * 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
+      dma16(vc + r * row + sw * 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
     }
     // Lanes 0-15: K scales of the 16 tokens, lanes 16-31: V scales (lanes
     // 32-63 repeat them into unused bytes).
     const float* sc = (lane & 16) ? p.v_scale : p.k_scale;
-    dma4(sc + (slot0 + (lane & 15)) * p.hkv + m.h, dst + 4096);
+    dma4(sc + (live ? (slot0 + (lane & 15)) * p.hkv + m.h : 0), dst + 4096);
   }
 }
 
@@ -553,19 +576,29 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
   const int n = lane & 15, g = lane >> 4;
   uint8_t* vt = FP8 ? stg : stg + DT * ROWB;  // bf16 V tile (E4M3FN: decoded over the code bytes)
 
+  // V^T operand: source lane n of group g reads row 4g + n/4, d = 16dt + 4(n%4).
+  const int r0 = 4 * g + (n >> 2);
+  // bf16: every LDS operand read of the step (4 K, 8 V^T fragments) is issued
+  // before the first MFMA, so the step pays one LDS round trip.
+  s16x4 va[8];
+  if constexpr (!FP8) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
+  }
   // S^T = K Q^T for the 16 tokens: k-step kk covers d = 32kk + 8g + {0..7}.
-  f32x4 s = f32x4{0, 0, 0, 0};
+  u32x4 a[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    u32x4 a;
     if constexpr (FP8) {
       const int c = 2 * kk + (g >> 1);
-      a = fp8x8_to_bf16x8(ld8(stg + n * 128 + 16 * (c ^ (n & 7)) + 8 * (g & 1)));
+      a[kk] = fp8x8_to_bf16x8(ld8(stg + n * 128 + 16 * (c ^ (n & 7)) + 8 * (g & 1)));
     } else {
-      a = ld16(stg + k_off(n, 4 * kk + g));
+      a[kk] = ld16(stg + k_off(n, 4 * kk + g));
     }
-    s = mfma16(as_bf16x8(a), as_bf16x8(qv[kk]), s);
   }
+  f32x4 s = f32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) s = mfma16(as_bf16x8(a[kk]), as_bf16x8(qv[kk]), s);
 
   if constexpr (FP8) {
     // V codes -> bf16 tile over the code bytes: lane covers row lane/4, 32 bytes
@@ -580,10 +613,15 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
     st16(vt + v_off(r, 4 * seg + 2), fp8x8_to_bf16x8(u32x2{w1.x, w1.y}));
     st16(vt + v_off(r, 4 * seg + 3), fp8x8_to_bf16x8(u32x2{w1.z, w1.w}));
   } else if (ntok < DT) {
-    // Rows past the valid tokens become zeros (the step has landed).
+    // V rows past the valid tokens (whatever the pool holds there) become
+    // zeros in the operand: lane (n, g) holds tokens 4g + {0..3}.
+    const uint32_t m01 = (4 * g + 0 < ntok ? 0xffffu : 0u) | (4 * g + 1 < ntok ? 0xffff0000u : 0u);
+    const uint32_t m23 = (4 * g + 2 < ntok ? 0xffffu : 0u) | (4 * g + 3 < ntok ? 0xffff0000u : 0u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (4 * i + g >= ntok) st16(vt + (4 * i + g) * ROWB + (n << 4), u32x4{0, 0, 0, 0});
+    for (int dt = 0; dt < 8; ++dt) {
+      const u32x2 w = __builtin_bit_cast(u32x2, va[dt]);
+      va[dt] = __builtin_bit_cast(s16x4, u32x2{w.x & m01, w.y & m23});
+    }
   }
 
   f32x4 ksc = f32x4{1, 1, 1, 1}, vsc = f32x4{1, 1, 1, 1};
@@ -601,9 +639,12 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
     mx = fmaxf(mx, x[i]);
   }
   mx = col_max(mx);
-  const float mnew = fmaxf(m, mx);
+  // Lazy offset (as in the prefill softmax): it moves only by more than
+  // 2^RESCALE_LOG2, so e <= 2^RESCALE_LOG2 and O is rarely rescaled.
+  const bool grow = mx - m > RESCALE_LOG2;  // false when both are -inf
+  const float mnew = grow ? mx : m;
   const float mu = mnew == NEG_INF ? 0.0f : mnew;
-  const float alpha = __builtin_amdgcn_exp2f(m - mu);
+  const float alpha = grow ? __builtin_amdgcn_exp2f(m - mu) : 1.0f;
   float e[4], rs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -614,28 +655,30 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
   rs = col_sum(rs);
   l = l * alpha + rs;
   m = mnew;
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+  if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
   }
   // P^T as the B operand of the 16x16x16 product: k slot (g, j) is token 4g + j.
   const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])});
-  // V^T operand: source lane n of group g reads row 4g + n/4, d = 16dt + 4(n%4).
-  const int r0 = 4 * g + (n >> 2);
+  if constexpr (FP8) {  // the decoded tile is read only now
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-    const s16x4 va = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
-    o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dt], 0, 0, 0);
+    for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
   }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt], 0, 0, 0);
 }
 
 // Cross-wavefront merge.  Per pass of 4 query heads, every wavefront writes
 // its accumulators into its own stage-1 region (idle between its last step
 // and the next item's step-1 loads) and its (m, l) into the merge area; after
 // a barrier, wavefront w combines query head 4*pass + w over the four
-// wavefronts and writes the output (single chunk) or the chunk's split-K
-// partial.  Entered after a barrier that follows every wavefront's last step;
-// ends with a barrier, after which the stage-1 regions may take new loads.
+// wavefronts (lane j < 32 owns d = 4j..4j+3) and writes the output (single
+// chunk) or the chunk's split-K record [acc | m, l] (lane 32 holds m, l).
+// Every wavefront issues exactly one store instruction per pass (to the trash
+// line when it has no head), so the decode loop's waits can count them.
+// Entered after a barrier that follows every wavefront's last step; ends with
+// a barrier, after which the stage-1 regions may take new loads.
 __device__ __forceinline__ void decode_merge(const Params& p, Smem& sm, uint8_t* st1, const DMeta& md, int tid,
                                              const f32x4 (&o)[8], float mx, float ls) {
   const int lane = tid & 63, wave = tid >> 6;
@@ -656,31 +699,31 @@ __device__ __forceinline__ void decode_merge(const Params& p, Smem& sm, uint8_t*
     }
     lds_sync();
     const int hn = hg + wave;
-    if (hn < G) {
-      float M = NEG_INF;
+    const int j = lane & 31;
+    if (hn >= G) {
+      if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
+      continue;
+    }
+    float M = NEG_INF;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.u.dec.m[w][wave]);
-      float Ls = 0.0f;
-      float2 acc = make_float2(0.0f, 0.0f);
-      const int d = 2 * lane;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm.u.dec.m[w][wave]);
+    float Ls = 0.0f;
+    f32x4 acc = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float mw = sm.u.dec.m[w][wave];
-        const float f = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-        Ls += f * sm.u.dec.l[w][wave];
-        const float2 v = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(st1 + w * WSTAGE) +
-                                                          wave * HD + d);
-        acc.x += f * v.x;
-        acc.y += f * v.y;
-      }
-      if (nch == 1) {
-        const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-        store4(p.out + (int64_t)md.b * p.out_stride + (int64_t)(md.h * G + hn) * HD + d,
-               pack_bf16x2(acc.x * inv, acc.y * inv));
-      } else {
-        store8_agent(part + hn * HD + d, u32x2{__float_as_uint(acc.x), __float_as_uint(acc.y)});
-        if (lane == 0) store8_agent(part + G * HD + 4 * hn, u32x2{__float_as_uint(M), __float_as_uint(Ls)});
-      }
+    for (int w = 0; w < 4; ++w) {
+      const float mw = sm.u.dec.m[w][wave];
+      const float f = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      Ls += f * sm.u.dec.l[w][wave];
+      acc += f * *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(st1 + w * WSTAGE) + wave * HD + 4 * j);
+    }
+    if (nch == 1) {
+      const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+      if (lane < 32)
+        store8(p.out + (int64_t)md.b * p.out_stride + (int64_t)(md.h * G + hn) * HD + 4 * j,
+               u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)});
+    } else if (lane < 33) {
+      const f32x4 v = lane < 32 ? acc : f32x4{M, Ls, 0.0f, 0.0f};
+      store16_agent(part + hn * PREC + 4 * lane, __builtin_bit_cast(u32x4, v));
     }
   }
   lds_sync();
@@ -708,8 +751,8 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
       for (int k = 0; k < 16; ++k) {
         const bool ok = c0 + k < nch;
         const float* pc = p0 + (size_t)(ok ? c0 + k : c0) * pstride;
-        ml[k] = ok ? load_partial2(pc + G * HD + 4 * hn) : make_float2(NEG_INF, 0.0f);
-        ov[k] = ok ? load_partial2(pc + hn * HD + d) : make_float2(0.0f, 0.0f);
+        ml[k] = ok ? load_partial2(pc + hn * PREC + HD) : make_float2(NEG_INF, 0.0f);
+        ov[k] = ok ? load_partial2(pc + hn * PREC + d) : make_float2(0.0f, 0.0f);
       }
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
@@ -762,95 +805,172 @@ __device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int 
     const int nch = max(1, (L + CHUNK - 1) / CHUNK);
     if (nch == 1) continue;
     int* ticket = &p.counters[b * p.hkv + h];
-    if (tid == 0)
-      while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nch) __builtin_amdgcn_s_sleep(2);
+    // Bounded wait: a ticket that never completes (an inconsistent workspace)
+    // raises the fault word and lets the launch end instead of hanging.
+    if (tid == 0) {
+      int spins = 0;
+      while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nch) {
+        if (++spins > SPIN_LIMIT) {
+          store4(p.ctrl + FAULT_WORD, 1u);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
     lds_sync();
     decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, nch, tid);
   }
 }
 
+// s_waitcnt vmcnt(base + extra) for a small runtime `extra` (0..7).
+template <int BASE>
+__device__ __forceinline__ void wait_vm(int extra) {
+  switch (extra) {
+    case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 6)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(BASE + 7)); break;
+  }
+}
+
 // Runs this workgroup's remaining items, all decode items, starting with
 // relative index rel0 (row r0), and returns with sm.item holding the last
-// (out-of-list) fetch result.  Every fetch issued is consumed, and none is
-// issued after an out-of-list one.
+// in-list or out-of-list fetch result.  Every fetch issued is consumed, and
+// none is issued after an out-of-list one (later ones add 0).
+//
+// Vector memory operations of item k (cur), in issue order; G = step loads per
+// wavefront, H = merge stores per wavefront, [0] = wavefront 0 only:
+//   step 0: [0] fetch (claims the item after nxt)     step (cur, 2)
+//   step 1: [0] ticket of prev   Q(nxt)                step (cur, 3)
+//   step 2: step (nxt, 0)   [0] metadata of the item after nxt
+//   step 3: merge stores (H)   step (nxt, 1)
+// so the waits before steps 0..3 allow H+G+[1], G+[1], G+1+[1], G+[1] younger
+// operations.
 template <bool FP8>
 __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
                            uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
                            int r0, int tid) {
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  uint8_t* sa = st0 + wave * WSTAGE;  // step 0 of every item
-  uint8_t* sb = st1 + wave * WSTAGE;  // step 1
+  const bool w0 = wave == 0;
+  const int x0 = w0 ? 1 : 0;
+  uint8_t* sa = st0 + wave * WSTAGE;  // even steps
+  uint8_t* sb = st1 + wave * WSTAGE;  // odd steps
   constexpr int GROUP = d_group<FP8>();
+  const int hgp = (p.G + 3) >> 2;  // merge stores per wavefront and item
+  auto item_of = [&](uint32_t rel) { return decode_base + list + (int)rel * nlist; };
 
+  // Prologue: the first item's metadata and the fetch of the item after it,
+  // then the same operations the loop's last step leaves in flight.
+  DMeta cur = decode_geom(p, r0, __builtin_amdgcn_readfirstlane(item_of(rel0) - sm.off[r0]), item_of(rel0), decode_base);
   uint32_t f = 0;
-  if (tid == 0) f = atomic_add_ret(ctr, 1u);  // issued before the loads, so its wait drains nothing
-  DMeta cur = decode_meta(p, sm, decode_base + list + (int)rel0 * nlist, r0, decode_base);
-  decode_issue_q(p, qbuf, cur, wave, lane);
-  decode_issue<FP8>(p, sa, cur, 0, wave, lane);
-  decode_issue<FP8>(p, sb, cur, 1, wave, lane);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(1 + 2 * GROUP));  // the fetch (and nothing issued after it)
+  if (tid == 0) f = atomic_add_ret(ctr, 1u);
+  if (w0) decode_meta_dma(p, sm, cur, 0, lane);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   if (tid == 0) sm.item = after_wait(f) - base;
   lds_sync();
-  uint32_t rel = __builtin_amdgcn_readfirstlane(sm.item);
-  bool has_next = rel < count;
+  decode_meta_read(cur, sm, 0);
+  bool has1 = __builtin_amdgcn_readfirstlane(sm.item) < count;  // nxt exists
   DMeta nxt = cur;
-  if (has_next) {
-    const int item = decode_base + list + (int)rel * nlist;
-    nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
+  if (has1) {
+    const int item = item_of(__builtin_amdgcn_readfirstlane(sm.item));
+    const int r = find_row(sm, item, p.np, nrows, lane);
+    nxt = decode_geom(p, r, __builtin_amdgcn_readfirstlane(item - sm.off[r]), item, decode_base);
   }
+  decode_issue_q(p, qbuf, cur, wave, lane);
+  decode_issue<FP8>(p, sa, cur, 0, wave, lane);
+  if (w0) decode_meta_dma(p, sm, nxt, 1, lane);
+  for (int i = 0; i < hgp; ++i)
+    if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
+  decode_issue<FP8>(p, sb, cur, 1, wave, lane);
 
-  DMeta prev = cur;         // item whose partial was stored last
-  bool ticket_due = false;  // prev's partial is stored and its ticket not yet taken
-  for (;;) {
-    // Step 0: Q and step 0 landed; only step 1 (GROUP loads) may be in flight.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
-    lds_sync();  // every wavefront's quarter of Q has landed
+  DMeta prev = cur;
+  bool due = false;  // prev's partial is stored and its ticket not yet taken
+  for (int k = 0;; ++k) {
+    const uint8_t* qcur = qbuf + (k & 1) * QBUF;
+    uint8_t* qnxt = qbuf + ((k + 1) & 1) * QBUF;
+
+    // Step 0: (cur, 0) and Q(cur) have landed.
+    wait_vm<GROUP>(hgp + x0);
+    lds_sync();
     u32x4 qv[4];
     {
       const int hn = min(n, p.G - 1);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qbuf + hn * ROWB + 16 * (4 * kk + g));
+      for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qcur + hn * ROWB + 16 * (4 * kk + g));
     }
-    // Every wavefront's partial stores of the previous item are complete (each
-    // waited past them, then the barrier): its ticket goes out.  The next
-    // fetch goes out here too; its result is read after step 1's wait.
-    if (tid == 0 && ticket_due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
-    ticket_due = false;
-    if (tid == 0 && has_next) f = atomic_add_ret(ctr, 1u);
-
+    if (tid == 0) f = atomic_add_ret(ctr, has1 ? 1u : 0u);
     f32x4 o[8];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
     float m = NEG_INF, l = 0.0f;
     decode_step<FP8>(p, sa, decode_ntok(p, cur, 0, wave), qv, o, m, l, lane);
-    decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
+    decode_issue<FP8>(p, sa, cur, 2, wave, lane);
 
-    // Step 1: only the next item's step 0 may be in flight.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
+    // Step 1: (cur, 1) has landed, and with it prev's stores (every
+    // wavefront's, after the barrier) and nxt's metadata.
+    wait_vm<GROUP>(x0);
+    lds_sync();
+    if (has1) decode_meta_read(nxt, sm, (k + 1) & 1);
+    if (tid == 0) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], due ? 1u : 0u);
+    due = false;
+    decode_issue_q(p, qnxt, nxt, wave, lane);
     decode_step<FP8>(p, sb, decode_ntok(p, cur, 1, wave), qv, o, m, l, lane);
+    decode_issue<FP8>(p, sb, cur, 3, wave, lane);
 
-    lds_sync();  // every wavefront is done with Q and the merge area
-    decode_issue_q(p, qbuf, nxt, wave, lane);
-    // The fetch was issued before the loads step 1 waited past.
-    if (tid == 0 && has_next) sm.item = after_wait(f) - base;
+    // Step 2: (cur, 2) and the fetch have landed.  Wavefront 0 finds the
+    // fetched item's row, broadcasts it and loads the item's metadata.
+    wait_vm<GROUP + 1>(x0);
+    bool has2 = false;
+    DMeta nxt2 = nxt;
+    if (w0 && has1) {
+      const uint32_t rel2 = __builtin_amdgcn_readfirstlane(after_wait(f)) - base;
+      has2 = rel2 < count;
+      if (has2) {
+        const int item = item_of(rel2);
+        const int r = find_row(sm, item, p.np, nrows, lane);
+        const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
+        nxt2 = decode_geom(p, r, local, item, decode_base);
+        if (tid == 0) {
+          sm.bcast[0] = r;
+          sm.bcast[1] = local;
+        }
+      }
+      if (tid == 0) sm.item = rel2;
+    }
+    decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
+    decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
+    if (w0) decode_meta_dma(p, sm, has2 ? nxt2 : nxt, k & 1, lane);
+
+    // Step 3: (cur, 3) has landed; the broadcast is visible after the barrier.
+    wait_vm<GROUP>(x0);
+    lds_sync();
+    if (has1 && !w0) {
+      const uint32_t rel2 = __builtin_amdgcn_readfirstlane(sm.item);
+      has2 = rel2 < count;
+      if (has2)
+        nxt2 = decode_geom(p, __builtin_amdgcn_readfirstlane(sm.bcast[0]), __builtin_amdgcn_readfirstlane(sm.bcast[1]),
+                           item_of(rel2), decode_base);
+    }
+    decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
+    lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
     decode_issue<FP8>(p, sb, nxt, 1, wave, lane);
     prev = cur;
-    ticket_due = decode_nch(p, cur) > 1;
-    if (!has_next) break;
+    due = decode_nch(p, cur) > 1;
+    if (!has1) break;
     cur = nxt;
-    rel = __builtin_amdgcn_readfirstlane(sm.item);
-    has_next = rel < count;
-    if (has_next) {
-      const int item = decode_base + list + (int)rel * nlist;
-      nxt = decode_meta(p, sm, item, find_row(sm, item, p.np, nrows, lane), decode_base);
-    }
+    if (has2) nxt = nxt2;
+    has1 = has2;
   }
-  // The last item's partial stores (and the repeated loads) complete here.
+  // The last item's stores (and the repeated loads) complete here.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   lds_sync();
-  if (tid == 0 && ticket_due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
+  if (tid == 0 && due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
 }
 
 // --------------------------------------------------------------- prefill item
@@ -1123,7 +1243,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   __shared__ Smem sm;
   __shared__ __attribute__((aligned(16))) uint8_t stage0[STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t stage1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t qbuf[MAX_G * HD * 2];  // decode: Q of the current item
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[2 * QBUF];  // decode: Q of the current and next item
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
@@ -1190,8 +1310,8 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // i % nlist of that family and workgroup b serves list b % nlist of both, so
   // the lists' fetch counters are separate addresses (and, with round-robin
   // dispatch and 8 kv heads, one kv head's prefill tiles stay on one XCD's
-  // L2).  Alternate workgroups of a list start with different families and
-  // take the other one when theirs is exhausted, so MFMA-bound prefill items
+  // L2).  Workgroups of a list start with different families and take the
+  // other one when theirs is exhausted, so MFMA-bound prefill items
   // and HBM-bound decode items run side by side from the start.  A list's
   // counter only grows; the list's base is the counter value at which this
   // launch's items start.  Every workgroup reads the base before its first
@@ -1202,7 +1322,12 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   const int nlist = min((int)gridDim.x, NLIST);
   const int list = blockIdx.x % nlist;
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
-  const int first = (blockIdx.x / nlist) & 1;  // family taken first: 0 prefill, 1 decode
+  // Family taken first (0 prefill, 1 decode): the first half of the grid
+  // starts with prefill, the second with decode.  The dispatcher fills every
+  // CU's first workgroup slot before any second one, so workgroups b and
+  // b + grid/2 share a CU and each CU pairs an MFMA-bound prefill workgroup
+  // with an HBM-bound decode one.
+  const int first = 2 * (int)blockIdx.x >= (int)gridDim.x ? 1 : 0;
   if (tid == 0) sm.salt = 0;
   for (int pass = 0; pass < 2; ++pass) {
     const int fam = first ^ pass;
