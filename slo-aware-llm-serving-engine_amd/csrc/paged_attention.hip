@@ -65,6 +65,7 @@ constexpr int HD = 128;                // head_dim this kernel implements
 constexpr int NT = 256;                // threads per workgroup (4 wavefronts)
 constexpr int TT = 64;                 // tokens per tile
 constexpr int CHUNK = 256;             // decode split-K chunk (tokens): four workgroup steps
+constexpr int CHUNK_MIN = 128;         // chunk of launches with few decode tokens (two live steps)
 constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
 constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
 constexpr int BQ_MIN = 16;             // query positions per prefill item: 16 or 32 (per launch)
@@ -150,6 +151,7 @@ struct Smem {
   int off[MAX_ROWS + 1];
   int wsum[4];
   int wmax[4];
+  int dsum[4];
   uint32_t item;
   uint32_t base;
   int row;
@@ -329,13 +331,13 @@ __device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& 
   work = nqb * max(mean, 1) * p.hkv * p.HG;
 }
 
-__device__ __forceinline__ int row_items(const Params& p, int r, int bq) {
+__device__ __forceinline__ int row_items(const Params& p, int r, int bq, int dchunk) {
   if (r < p.np) {
     const int lq = p.cu_q[r + 1] - p.cu_q[r];
     return lq > 0 ? ((lq + bq - 1) / bq) * p.hkv * p.HG : 0;
   }
   const int L = decode_len(p, r - p.np);
-  return max(1, (L + CHUNK - 1) / CHUNK) * p.hkv;
+  return max(1, (L + dchunk - 1) / dchunk) * p.hkv;
 }
 
 __device__ __forceinline__ void store_partial(float* p, float v) {
@@ -445,6 +447,7 @@ __device__ __forceinline__ void lds_sync() {
 
 struct DMeta {
   int b, h, c, dindex;  // wave-uniform
+  int tok0, span;       // first token of the item, tokens per item (the launch's chunk)
   int len;              // dlens[b] as read (clamped where used)
   int page[NSTEP];      // KV block of each workgroup step
 };
@@ -453,16 +456,19 @@ __device__ __forceinline__ int decode_L(const Params& p, const DMeta& m) {
   return min(max(m.len, 0), p.dtab_width * p.block_size);
 }
 __device__ __forceinline__ int decode_nch(const Params& p, const DMeta& m) {
-  return max(1, (decode_L(p, m) + CHUNK - 1) / CHUNK);
+  return max(1, (decode_L(p, m) + m.span - 1) / m.span);
 }
 
 // Item geometry from its row and index within the row.
-__device__ __forceinline__ DMeta decode_geom(const Params& p, int r, int local, int item, int decode_base) {
+__device__ __forceinline__ DMeta decode_geom(const Params& p, int r, int local, int item, int decode_base,
+                                             int dchunk) {
   DMeta m;
   m.b = r - p.np;
   m.h = local % p.hkv;
   m.c = local / p.hkv;
   m.dindex = item - decode_base;
+  m.span = dchunk;
+  m.tok0 = m.c * dchunk;
   m.len = 0;
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) m.page[s] = -1;
@@ -477,7 +483,7 @@ __device__ __forceinline__ void decode_meta_dma(const Params& p, Smem& sm, const
   const int s = lane - 1;
   const int32_t* src =
       (s >= 0 && s < NSTEP)
-          ? p.dtab + (int64_t)m.b * p.dtab_stride + min((m.c * CHUNK + s * DSTEP) / p.block_size, p.dtab_width - 1)
+          ? p.dtab + (int64_t)m.b * p.dtab_stride + min((m.tok0 + s * DSTEP) / p.block_size, p.dtab_width - 1)
           : p.dlens + m.b;
   if (lane <= NSTEP) dma4(src, lds_addr(sm.meta[slot]));
 }
@@ -499,11 +505,12 @@ __device__ __forceinline__ int find_row(const Smem& sm, int item, int lo, int nr
   return -1;
 }
 
-// Valid tokens of wavefront `wave` in step s of the item (0 for padding blocks).
+// Valid tokens of wavefront `wave` in step s of the item (0 for padding
+// blocks and for steps past the item's span).
 __device__ __forceinline__ int decode_ntok(const Params& p, const DMeta& m, int s, int wave) {
   const int page = m.page[s];
-  if (page < 0 || page >= p.num_blocks) return 0;
-  return min(max(decode_L(p, m) - (m.c * CHUNK + s * DSTEP + wave * DT), 0), DT);
+  if (page < 0 || page >= p.num_blocks || s * DSTEP >= m.span) return 0;
+  return min(max(decode_L(p, m) - (m.tok0 + s * DSTEP + wave * DT), 0), DT);
 }
 
 // The item's G query heads (G*HD bf16, contiguous in the row) to qbuf; each
@@ -525,7 +532,7 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
                                              int lane) {
   const int n = lane & 15, g = lane >> 4;
   const int ntok = decode_ntok(p, m, s, wave);
-  const int t0 = m.c * CHUNK + s * DSTEP + wave * DT;
+  const int t0 = m.tok0 + s * DSTEP + wave * DT;
   // A step without valid tokens loads the pool's first line on every lane.
   const bool live = ntok > 0;
   const int64_t slot0 = live ? (int64_t)m.page[s] * p.block_size + t0 % p.block_size : 0;
@@ -781,7 +788,7 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // tasks), merges, and resets the ticket for the next launch.  Like the work
 // lists, a counter only grows: a launch makes exactly tasks + workgroups
 // fetches on it, and the workgroup making the last one advances its base.
-__device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int tid) {
+__device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
   uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (2 * NLIST + list) * CTRL_STRIDE;
   const int ntask = p.nd * p.hkv;
   const uint32_t count = list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u;
@@ -802,7 +809,7 @@ __device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int 
     const int task = list + (int)rel * nlist;
     const int b = task / p.hkv, h = task % p.hkv;
     const int L = min(max(p.dlens[b], 0), p.dtab_width * p.block_size);
-    const int nch = max(1, (L + CHUNK - 1) / CHUNK);
+    const int nch = max(1, (L + dchunk - 1) / dchunk);
     if (nch == 1) continue;
     int* ticket = &p.counters[b * p.hkv + h];
     // Bounded wait: a ticket that never completes (an inconsistent workspace)
@@ -853,10 +860,11 @@ __device__ __forceinline__ void wait_vm(int extra) {
 template <bool FP8>
 __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
                            uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
-                           int r0, int tid) {
+                           int r0, int dchunk, int tid) {
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const bool w0 = wave == 0;
+  const bool half = dchunk < CHUNK;  // steps 2 and 3 of every item are empty
   const int x0 = w0 ? 1 : 0;
   uint8_t* sa = st0 + wave * WSTAGE;  // even steps
   uint8_t* sb = st1 + wave * WSTAGE;  // odd steps
@@ -866,7 +874,8 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 
   // Prologue: the first item's metadata and the fetch of the item after it,
   // then the same operations the loop's last step leaves in flight.
-  DMeta cur = decode_geom(p, r0, __builtin_amdgcn_readfirstlane(item_of(rel0) - sm.off[r0]), item_of(rel0), decode_base);
+  DMeta cur = decode_geom(p, r0, __builtin_amdgcn_readfirstlane(item_of(rel0) - sm.off[r0]), item_of(rel0), decode_base,
+                          dchunk);
   uint32_t f = 0;
   if (tid == 0) f = atomic_add_ret(ctr, 1u);
   if (w0) decode_meta_dma(p, sm, cur, 0, lane);
@@ -879,7 +888,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   if (has1) {
     const int item = item_of(__builtin_amdgcn_readfirstlane(sm.item));
     const int r = find_row(sm, item, p.np, nrows, lane);
-    nxt = decode_geom(p, r, __builtin_amdgcn_readfirstlane(item - sm.off[r]), item, decode_base);
+    nxt = decode_geom(p, r, __builtin_amdgcn_readfirstlane(item - sm.off[r]), item, decode_base, dchunk);
   }
   decode_issue_q(p, qbuf, cur, wave, lane);
   decode_issue<FP8>(p, sa, cur, 0, wave, lane);
@@ -934,7 +943,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
         const int item = item_of(rel2);
         const int r = find_row(sm, item, p.np, nrows, lane);
         const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
-        nxt2 = decode_geom(p, r, local, item, decode_base);
+        nxt2 = decode_geom(p, r, local, item, decode_base, dchunk);
         if (tid == 0) {
           sm.bcast[0] = r;
           sm.bcast[1] = local;
@@ -942,7 +951,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       }
       if (tid == 0) sm.item = rel2;
     }
-    decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
+    if (!half) decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
     decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
     if (w0) decode_meta_dma(p, sm, has2 ? nxt2 : nxt, k & 1, lane);
 
@@ -954,9 +963,9 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       has2 = rel2 < count;
       if (has2)
         nxt2 = decode_geom(p, __builtin_amdgcn_readfirstlane(sm.bcast[0]), __builtin_amdgcn_readfirstlane(sm.bcast[1]),
-                           item_of(rel2), decode_base);
+                           item_of(rel2), decode_base, dchunk);
     }
-    decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
+    if (!half) decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
     decode_issue<FP8>(p, sb, nxt, 1, wave, lane);
@@ -1252,40 +1261,51 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 
   // Prefill block size: 16 query positions when the heaviest 32-position
   // block would take more than twice a workgroup's fair share of the prefill
-  // work (the launch would wait on that one item), else 32.
-  int bq = 32;
-  if (p.np > 0) {
-    int w = 0, tm = 0;
-    for (int r = r0; r < min(r0 + per, p.np); ++r) {
-      int wr, tr;
-      pf_work(p, r, wr, tr);
-      w += wr;
-      tm = max(tm, tr);
+  // work (the launch would wait on that one item), else 32.  Decode chunk:
+  // CHUNK tokens when that still gives at least two items per workgroup,
+  // else CHUNK_MIN (short launches need the parallelism more than the longer
+  // items' lower per-token overhead).
+  int bq = 32, dchunk = CHUNK;
+  {
+    int w = 0, tm = 0, dn = 0;
+    for (int r = r0; r < min(r0 + per, nrows); ++r) {
+      if (r < p.np) {
+        int wr, tr;
+        pf_work(p, r, wr, tr);
+        w += wr;
+        tm = max(tm, tr);
+      } else {
+        dn += (decode_len(p, r - p.np) + CHUNK - 1) / CHUNK;
+      }
     }
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       w += __shfl_xor(w, d, 64);
       tm = max(tm, __shfl_xor(tm, d, 64));
+      dn += __shfl_xor(dn, d, 64);
     }
     if (lane == 0) {
       sm.wsum[wave] = w;
       sm.wmax[wave] = tm;
+      sm.dsum[wave] = dn;
     }
     __syncthreads();
-    int64_t wt = 0;
+    int64_t wt = 0, dt = 0;
     int tmax = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       wt += sm.wsum[i];
       tmax = max(tmax, sm.wmax[i]);
+      dt += sm.dsum[i];
     }
-    if ((int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
+    if (p.np > 0 && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
+    if (dt * p.hkv < 2 * (int64_t)gridDim.x) dchunk = CHUNK_MIN;
     __syncthreads();
   }
 
   // Per-row item counts -> exclusive prefix in sm.off (block-wide scan).
   int local_sum = 0;
-  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r, bq);
+  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r, bq, dchunk);
   int incl = local_sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -1298,7 +1318,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   for (int w = 0; w < wave; ++w) run += sm.wsum[w];
   for (int r = r0; r < min(r0 + per, nrows); ++r) {
     sm.off[r] = run;
-    run += row_items(p, r, bq);
+    run += row_items(p, r, bq, dchunk);
   }
   if (tid == NT - 1) sm.off[nrows] = run;
   __syncthreads();
@@ -1383,14 +1403,15 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
         continue;
       }
       // The rest of this decode list is one streaming decode run.
-      decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, ltid);
+      decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, dchunk,
+                      ltid);
       break;
     }
     if (tid == 0 && sm.item == count + wgs - 1u)
       __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
-  if (p.nd > 0) merge_tasks(p, sm, list, nlist, decode_base, tid);
+  if (p.nd > 0) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
 }
 
 struct DeviceShape {
@@ -1435,7 +1456,7 @@ extern "C" int slo_attention_workspace_bytes(int32_t max_decode_rows, int32_t ma
       num_heads % num_kv_heads)
     return fail(SLO_ERR_INVALID, "workspace_bytes: bad arguments");
   if (head_dim != HD) return fail(SLO_ERR_UNSUPPORTED, "workspace_bytes: head_dim must be 128");
-  const int64_t chunks = (max_decode_len + CHUNK - 1) / CHUNK;
+  const int64_t chunks = (max_decode_len + CHUNK_MIN - 1) / CHUNK_MIN;
   const int64_t items = (int64_t)max_decode_rows * std::max<int64_t>(1, chunks) * num_kv_heads;
   *bytes = PARTIALS_OFFSET + sizeof(float) * partial_floats(items, num_heads / num_kv_heads);
   return SLO_OK;
@@ -1539,7 +1560,7 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
 
   // Upper bound on the item count from host-known shapes only.
   int64_t bound = 0;
-  if (do_dec) bound += (int64_t)p.nd * ((dec_len_cap + CHUNK - 1) / CHUNK) * p.hkv;
+  if (do_dec) bound += (int64_t)p.nd * ((dec_len_cap + CHUNK_MIN - 1) / CHUNK_MIN) * p.hkv;
   if (do_pf) {
     const int64_t tq = std::max<int64_t>(0, a->num_q_rows - a->num_decode);
     bound += (tq / BQ_MIN + p.np) * p.hkv * p.HG;

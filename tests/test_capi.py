@@ -38,9 +38,9 @@ def test_workspace_bytes_and_errors():
     n2 = _lib.workspace_bytes(48, 4096, 32, 8, 128)
     n0 = _lib.workspace_bytes(0, 0, 32, 8, 128)
     # control lines + trash line + ticket array are fixed; partials grow with rows x chunks x heads:
-    # one record of G x (128 accumulators + m + l + 2 pad) floats per 256-token chunk
+    # one record of G x (128 accumulators + m + l + 2 pad) floats per chunk of at least 128 tokens
     per_item = 4 * (128 + 4) * 4
-    assert n2 - n1 == 24 * (4096 // 256) * 8 * per_item
+    assert n2 - n1 == 24 * (4096 // 128) * 8 * per_item
     assert n0 == 24 * 128 + 1024 + 4 * 65536
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.workspace_bytes(1, 1, 32, 8, 64)
