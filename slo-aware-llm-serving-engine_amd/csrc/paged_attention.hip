@@ -1247,21 +1247,34 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 }
 
 // ------------------------------------------------------------------- kernel
-template <bool FP8>
+// Launch shapes, one kernel instantiation each, so that every path is
+// register-allocated without the code of paths the launch cannot take.
+enum Mode : int {
+  MODE_MIXED = 0,    // decode and prefill rows; prefill in 32-position blocks
+  MODE_PREFILL = 1,  // prefill rows only; block size chosen per launch
+  MODE_DECODE = 2,   // decode rows only
+};
+
+template <bool FP8, int MODE>
 __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
+  constexpr bool HAS_DEC = MODE != MODE_PREFILL;
+  constexpr bool HAS_PF = MODE != MODE_DECODE;
   __shared__ Smem sm;
   __shared__ __attribute__((aligned(16))) uint8_t stage0[STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t stage1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t qbuf[2 * QBUF];  // decode: Q of the current and next item
+  // decode: Q of the current and next item
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[HAS_DEC ? 2 * QBUF : 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
   const int per = (nrows + NT - 1) / NT;
   const int r0 = tid * per;
 
-  // Prefill block size: 16 query positions when the heaviest 32-position
-  // block would take more than twice a workgroup's fair share of the prefill
-  // work (the launch would wait on that one item), else 32.  Decode chunk:
+  // Prefill block size: a launch with decode rows uses 32 query positions
+  // (the decode work hides the longest prefill item and 32 halves the key
+  // tiles loaded per query); a prefill-only launch uses 16 when the heaviest
+  // 32-position block would take more than twice a workgroup's fair share of
+  // the work (the launch would wait on that one item), else 32.  Decode chunk:
   // CHUNK tokens when that still gives at least two items per workgroup,
   // else CHUNK_MIN (short launches need the parallelism more than the longer
   // items' lower per-token overhead).
@@ -1298,7 +1311,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       tmax = max(tmax, sm.wmax[i]);
       dt += sm.dsum[i];
     }
-    if (p.np > 0 && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
+    if (MODE == MODE_PREFILL && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
     if (dt * p.hkv < 2 * (int64_t)gridDim.x) dchunk = CHUNK_MIN;
     __syncthreads();
   }
@@ -1389,10 +1402,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // the two item paths from being hoisted out of the loop, where they
       // would all stay live at once.
       const int ltid = tid + sm.salt;
-      if (r < p.np) {
+      if (HAS_PF && r < p.np) {
         const int item = list + (int)rel * nlist;
-        if (bq == 16) prefill_item<FP8, 1>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-        else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+        if constexpr (MODE == MODE_PREFILL) {
+          if (bq == 16) prefill_item<FP8, 1>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+        } else if constexpr (HAS_PF) {
+          prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+        }
         // The next item is fetched only now: fetching ahead would let a
         // workgroup claim a second item before a late-starting one takes its
         // first.
@@ -1403,15 +1420,16 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
         continue;
       }
       // The rest of this decode list is one streaming decode run.
-      decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r, dchunk,
-                      ltid);
+      if constexpr (HAS_DEC)
+        decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r,
+                        dchunk, ltid);
       break;
     }
     if (tid == 0 && sm.item == count + wgs - 1u)
       __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
-  if (p.nd > 0) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
+  if constexpr (HAS_DEC) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
 }
 
 struct DeviceShape {
@@ -1430,10 +1448,10 @@ int device_shape(DeviceShape* out) {
     DeviceShape s;
     if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return fail(SLO_ERR_HIP, "hipDeviceGetAttribute failed");
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[0], paged_attention_kernel<false>, NT, 0) !=
-            hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[1], paged_attention_kernel<true>, NT, 0) !=
-            hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[0], paged_attention_kernel<false, MODE_MIXED>, NT,
+                                                     0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[1], paged_attention_kernel<true, MODE_MIXED>, NT,
+                                                     0) != hipSuccess)
       return fail(SLO_ERR_HIP, "occupancy query failed");
     s.wg_per_cu[0] = std::max(1, s.wg_per_cu[0]);
     s.wg_per_cu[1] = std::max(1, s.wg_per_cu[1]);
@@ -1568,7 +1586,14 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8 ? 1 : 0];
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (fp8) hipLaunchKernelGGL((paged_attention_kernel<true>), dim3(grid), dim3(NT), 0, s, p);
-  else hipLaunchKernelGGL((paged_attention_kernel<false>), dim3(grid), dim3(NT), 0, s, p);
+  const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
+  switch (mode + 3 * (fp8 ? 1 : 0)) {
+    case 0: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_DECODE>), dim3(grid), dim3(NT), 0, s, p); break;
+    case 3: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;
+    default: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_DECODE>), dim3(grid), dim3(NT), 0, s, p); break;
+  }
   return check_launch("paged_attention");
 }
