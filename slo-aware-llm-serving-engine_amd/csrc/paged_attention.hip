@@ -27,13 +27,14 @@
 //    lane-local: the S^T accumulator is the B operand of the PV product
 //    without data movement, and V^T comes from the natural [token][d] LDS tile
 //    through ds_read_b64_tr_b16.
-//  * Decode item (row b, chunk of 128 tokens, kv head h): two workgroup steps
-//    of 64 tokens, 16 per wavefront; the G query heads sharing h are the MFMA
-//    columns.  K, V and Q go from HBM straight into LDS (global_load_lds) and
-//    two steps stay in flight per wavefront across item boundaries.  The 4
-//    wavefronts merge in LDS; a row with several chunks writes one
-//    (acc, m, l) partial per chunk, and after its own items every workgroup
-//    takes split-K merge tasks from its list, each waiting for the chunks of
+//  * Decode item (row b, chunk of 256 tokens, or 128 in launches with few
+//    decode tokens, kv head h): four workgroup steps of 64 tokens, 16 per
+//    wavefront; the G query heads sharing h are the MFMA columns.  K, V and Q
+//    go from HBM straight into LDS (global_load_lds) and two steps stay in
+//    flight per wavefront across item boundaries.  The 4 wavefronts merge in
+//    LDS; a row with several chunks writes one (acc, m, l) record per chunk,
+//    and after its own items every workgroup takes split-K merge tasks from
+//    its list, each waiting for the chunks of
 //    its (row, head) (the split-K merge of docs/project_manual.md:643-650).
 //
 // LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
