@@ -219,11 +219,6 @@ __device__ __forceinline__ float col_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Online-softmax update of one prefill tile for the wavefront's NQT query
-// columns.  Scores stay unscaled until the exponent: max commutes with the
-// positive factor c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA
-// and one v_exp_f32 per score.  `mask` selects the boundary-tile path (keys
-// past the tile's valid rows or causally after the column).
 // The running max used as the exponent offset moves only when a tile's max
 // exceeds it by more than 2^RESCALE_LOG2 (in units of the log2-scaled score),
 // so every probability stays <= 2^RESCALE_LOG2 (exact in bf16's range, far
@@ -231,68 +226,73 @@ __device__ __forceinline__ float col_sum(float x) {
 // tiles.  The result o / l is the same quantity as with an exact running max.
 constexpr float RESCALE_LOG2 = 8.0f;
 
-template <int NQT>
-__device__ __forceinline__ void prefill_softmax(f32x4 (&s)[4][NQT], float (&m)[NQT], float (&l)[NQT],
-                                                f32x4 (&o)[8][NQT], bf16x8 (&pb)[NQT][2], float c, bool src_fp8,
-                                                const float* ks, const float* vs, int g, bool mask, int ntok, int kv0,
-                                                int lim0) {
+// Online softmax of one half tile (32 keys: score blocks sh[0], sh[1] hold key
+// rows kh + 16*mm + 4g + i) for the wavefront's NQT query columns.  Scores stay
+// unscaled until the exponent: max commutes with the positive factor
+// c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA and one
+// v_exp_f32 per score; column reductions use v_permlane16/32_swap.  MASK
+// selects the boundary-tile path (keys past the tile's valid rows or causally
+// after the column).  Packs P^T into pb[nt] (the B operand of the half's PV
+// product) and returns in alpha[nt] the factor the accumulators must take
+// before that product; grow_any is set when any column's offset moved.
+// Branch-free for bf16 sources, so the compiler can interleave it with MFMA
+// work of the other half.
+template <int NQT, bool MASK>
+__device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT], float (&l)[NQT], float (&alpha)[NQT],
+                                             bool& grow_any, bf16x8 (&pb)[NQT], float c, bool src_fp8,
+                                             const float* ks, const float* vs, int g, int ntok, int kh, int kv0,
+                                             int lim0) {
+  uint64_t grows = 0;
 #pragma unroll
   for (int nt = 0; nt < NQT; ++nt) {
     if (src_fp8) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[mt][nt][i] *= ks[16 * mt + 4 * g + i];
+        for (int i = 0; i < 4; ++i) sh[mm][nt][i] *= ks[kh + 16 * mm + 4 * g + i];
     }
-    // Only tiles that reach past the valid keys or the block's causal edge
-    // are masked (a wave-uniform branch).
-    if (mask) {
-      const int lim = lim0 + 16 * nt;  // last visible key index of this column
+    if constexpr (MASK) {
+      const int lim = lim0 + 16 * nt;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int tok = 16 * mt + 4 * g + i;
-          s[mt][nt][i] = (tok < ntok && kv0 + tok <= lim) ? s[mt][nt][i] : NEG_INF;
+          const int tok = kh + 16 * mm + 4 * g + i;
+          sh[mm][nt][i] = (tok < ntok && kv0 + tok <= lim) ? sh[mm][nt][i] : NEG_INF;
         }
     }
     float mx = NEG_INF;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sh[mm][nt][i]);
     mx = col_max(mx);
-    // grow is false when both maxima are -inf (NaN compares false).
-    const bool grow = c * (mx - m[nt]) > RESCALE_LOG2;
+    const bool grow = c * (mx - m[nt]) > RESCALE_LOG2;  // false when both are -inf
     const float mnew = grow ? mx : m[nt];
     const float cm = mnew == NEG_INF ? 0.0f : c * mnew;
-    const float alpha = grow ? __builtin_amdgcn_exp2f(c * m[nt] - cm) : 1.0f;
+    const float a = grow ? __builtin_amdgcn_exp2f(c * m[nt] - cm) : 1.0f;
     float rs = 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][i], c, -cm));
+        const float e = __builtin_amdgcn_exp2f(fmaf(sh[mm][nt][i], c, -cm));
         rs += e;
-        s[mt][nt][i] = src_fp8 ? e * vs[16 * mt + 4 * g + i] : e;
+        sh[mm][nt][i] = src_fp8 ? e * vs[kh + 16 * mm + 4 * g + i] : e;
       }
     rs = col_sum(rs);
-    l[nt] = l[nt] * alpha + rs;
+    l[nt] = l[nt] * a + rs;
     m[nt] = mnew;
-    if (__builtin_amdgcn_ballot_w64(grow)) {  // no column's offset moved: skip the rescale
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt][nt] *= alpha;
-    }
-#pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      u32x4 w;
-      w.x = pack_bf16x2(s[2 * ks2][nt][0], s[2 * ks2][nt][1]);
-      w.y = pack_bf16x2(s[2 * ks2][nt][2], s[2 * ks2][nt][3]);
-      w.z = pack_bf16x2(s[2 * ks2 + 1][nt][0], s[2 * ks2 + 1][nt][1]);
-      w.w = pack_bf16x2(s[2 * ks2 + 1][nt][2], s[2 * ks2 + 1][nt][3]);
-      pb[nt][ks2] = as_bf16x8(w);
-    }
+    alpha[nt] = a;
+    grows |= __builtin_amdgcn_ballot_w64(grow);
+    u32x4 w;
+    w.x = pack_bf16x2(sh[0][nt][0], sh[0][nt][1]);
+    w.y = pack_bf16x2(sh[0][nt][2], sh[0][nt][3]);
+    w.z = pack_bf16x2(sh[1][nt][0], sh[1][nt][1]);
+    w.w = pack_bf16x2(sh[1][nt][2], sh[1][nt][3]);
+    pb[nt] = as_bf16x8(w);
   }
+  grow_any = grows != 0;
 }
 
 __device__ __forceinline__ int decode_len(const Params& p, int b) {
@@ -984,10 +984,6 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // --------------------------------------------------------------- prefill item
-#ifndef SLO_KB2
-#define SLO_KB2 8
-#endif
-constexpr int KB2 = SLO_KB2;  // LDS operand batch with two query blocks per wavefront
 template <bool FP8, int NQT>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
   constexpr int BQ = 16 * NQT;
@@ -1149,86 +1145,96 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     issue_tile(0, 0);
     commit_tile(0);
   }
-  for (int kv0 = 0, j = 0; kv0 < kend; kv0 += TT, ++j) {
+  // Each tile is processed as two halves of 32 keys,
+  // software-pipelined so that MFMA work of one half and the softmax VALU
+  // work of the other are independent and can be interleaved:
+  //   QK(h0);  QK(h1) | softmax(h0);  [rescale];  PV(h0) | softmax(h1);
+  //   [rescale];  PV(h1).
+  // The rescale of O (rare with the lazy offset) sits between the regions.
+  // Interior tiles (no key past the valid rows or the causal edge) run in a
+  // loop of their own without masking code.
+  auto tile = [&](auto mask_tag, int kv0, int j) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int buf = j & 1;
     const int ntok = min(TT, kend - kv0);
-    // This tile's DMA (the only one in flight) and register loads have
-    // landed; after the barrier every wavefront's part is visible and the
-    // other buffer is free.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     lds_sync();
     const bool more = kv0 + TT < kend;
     const uint8_t* kt = buf ? st1 : st0;
     const uint8_t* vt = kt + TILE_BYTES;
-    // The tile's MFMA operands are read from LDS in batches (all 16 K or V^T
-    // fragments with one query block, KB2 with two, where registers are
-    // short) so that one LDS round trip serves a batch, not a single MFMA.
-    // Fragment i of a batch is K rows 16*(i & 3) + n, k-step i >> 2.  With
-    // one query block the first V^T batch is read before the softmax.
-    constexpr int KB = NQT == 1 ? 16 : KB2;
-    constexpr bool VPRE = NQT == 1;
-    auto kread = [&](int i) { return ld16(kt + (i & 3) * 16 * ROWB + koff[i >> 2]); };
-    auto vread = [&](int i) {  // V^T operand: k-step i >> 3, d-tile i & 7
+    // K fragment jj of half h: rows 16*(2h + (jj & 1)) + n, k-step jj >> 1.
+    auto kread_h = [&](int h, int jj) { return ld16(kt + (2 * h + (jj & 1)) * 16 * ROWB + koff[jj >> 1]); };
+    auto vread = [&](int i) {  // V^T operand: k-step (half) i >> 3, d-tile i & 7
       const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
       return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
     };
-    u32x4 kf[KB];
+    u32x4 kf[8];
     if (active) {
 #pragma unroll
-      for (int i = 0; i < KB; ++i) kf[i] = kread(i);
+      for (int jj = 0; jj < 8; ++jj) kf[jj] = kread_h(0, jj);
     }
-    // The next tile's loads are issued while these reads are in flight.
     if (more) issue_tile(kv0 + TT, buf ^ 1);
     if (active) {
-      // S^T = K Q^T, four independent accumulator chains per query block.
-      f32x4 s[4][NQT];
+      f32x4 s0[2][NQT], s1[2][NQT];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-        for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = f32x4{0, 0, 0, 0};
+        for (int nt = 0; nt < NQT; ++nt) s0[mm][nt] = s1[mm][nt] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int b = 0; b < 16 / KB; ++b) {
-        if (b > 0) {
+      for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-          for (int i = 0; i < KB; ++i) kf[i] = kread(b * KB + i);
-        }
+        for (int nt = 0; nt < NQT; ++nt)
+          s0[jj & 1][nt] = mfma16(as_bf16x8(kf[jj]), as_bf16x8(qv[nt][jj >> 1]), s0[jj & 1][nt]);
 #pragma unroll
-        for (int i = 0; i < KB; ++i) {
-          const int j = b * KB + i, mt = j & 3, st = j >> 2;
-#pragma unroll
-          for (int nt = 0; nt < NQT; ++nt) s[mt][nt] = mfma16(as_bf16x8(kf[i]), as_bf16x8(qv[nt][st]), s[mt][nt]);
-        }
-      }
-      bf16x8 vf[KB];
-      if constexpr (VPRE) {
-#pragma unroll
-        for (int i = 0; i < KB; ++i) vf[i] = vread(i);
-      }
-
-      // Keys that can be masked: beyond the tile's valid rows, or causally
-      // after the earliest query column of the block.
-      const bool need_mask = ntok < TT || kv0 + TT - 1 > q0 + prefix;
-      bf16x8 pb[NQT][2];
+      for (int jj = 0; jj < 8; ++jj) kf[jj] = kread_h(1, jj);
       const int lim0 = q0 + n + prefix;
-      prefill_softmax<NQT>(s, m, l, o, pb, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, need_mask, ntok, kv0, lim0);
-
-      // O^T += V^T P^T.
+      float a0[NQT], a1[NQT];
+      bool g0, g1;
+      bf16x8 pb0[NQT], pb1[NQT];
 #pragma unroll
-      for (int b = 0; b < 16 / KB; ++b) {
-        if (b > 0 || !VPRE) {
+      for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-          for (int i = 0; i < KB; ++i) vf[i] = vread(b * KB + i);
-        }
+        for (int nt = 0; nt < NQT; ++nt)
+          s1[jj & 1][nt] = mfma16(as_bf16x8(kf[jj]), as_bf16x8(qv[nt][jj >> 1]), s1[jj & 1][nt]);
+      softmax_half<NQT, MASK>(s0, m, l, a0, g0, pb0, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
+                            0, kv0, lim0);
+      if (g0) {
 #pragma unroll
-        for (int i = 0; i < KB; ++i) {
-          const int j = b * KB + i;
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-          for (int nt = 0; nt < NQT; ++nt) o[j & 7][nt] = mfma16(vf[i], pb[nt][j >> 3], o[j & 7][nt]);
-        }
+          for (int nt = 0; nt < NQT; ++nt) o[dt][nt] *= a0[nt];
       }
+      bf16x8 vf[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vf[i] = vread(i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int nt = 0; nt < NQT; ++nt) o[i][nt] = mfma16(vf[i], pb0[nt], o[i][nt]);
+      softmax_half<NQT, MASK>(s1, m, l, a1, g1, pb1, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
+                            32, kv0, lim0);
+      if (g1) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+          for (int nt = 0; nt < NQT; ++nt) o[dt][nt] *= a1[nt];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vf[i] = vread(8 + i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int nt = 0; nt < NQT; ++nt) o[i][nt] = mfma16(vf[i], pb1[nt], o[i][nt]);
     }
     if (more) commit_tile(buf ^ 1);
-  }
+  };
+  // Tiles before the first one with a key past the valid rows or after the
+  // block's first query position (bottom-right causal) need no mask.
+  const int lim_first = min(kend - TT, q0 + prefix - (TT - 1));  // largest unmasked kv0
+  const int n_int = lim_first < 0 ? 0 : lim_first / TT + 1;
+  int kv0 = 0, j = 0;
+  for (; kv0 < kend && j < n_int; kv0 += TT, ++j) tile(std::integral_constant<bool, false>(), kv0, j);
+  for (; kv0 < kend; kv0 += TT, ++j) tile(std::integral_constant<bool, true>(), kv0, j);
 
   if (!active) return;
 #pragma unroll
