@@ -360,8 +360,8 @@ __device__ __forceinline__ float load_partial(const float* p) {
 //
 // Every vector memory operation of the loop (LDS DMA, atomics, split-K and
 // output stores) is issued through inline assembly at a fixed point, in the
-// same number on every pass: steps past the row's length still issue their
-// loads (all lanes of such a step read one cache line), after the last item
+// same number on every pass: a wavefront step past the row's length issues
+// its operations as single-lane 4-byte loads, after the last item
 // the next-item loads repeat the current item's, a ticket with nothing due
 // adds 0, a fetch after the list's end adds 0, and a wavefront without a query
 // head stores to a trash line.  Vector memory operations complete in issue
@@ -534,12 +534,19 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
   const int n = lane & 15, g = lane >> 4;
   const int ntok = decode_ntok(p, m, s, wave);
   const int t0 = m.tok0 + s * DSTEP + wave * DT;
-  // A step without valid tokens loads the pool's first line on every lane.
-  const bool live = ntok > 0;
-  const int64_t slot0 = live ? (int64_t)m.page[s] * p.block_size + t0 % p.block_size : 0;
-  const int row = live ? p.hkv * HD : 0;  // elements (bf16) or bytes (E4M3FN) between tokens
-  const int64_t base = live ? slot0 * row + (int64_t)m.h * HD : 0;
-  const int sw = live ? 1 : 0;  // keeps the swizzled chunk offsets only for live steps
+  if (ntok == 0) {
+    // A step without valid tokens issues the same number of operations, each
+    // a 4-byte load on one lane: counted like the others, nearly free.
+    const uint32_t dst = lds_addr(stg);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < d_group<FP8>(); ++i) dma4(p.dlens, dst + 4 * i);
+    }
+    return;
+  }
+  const int64_t slot0 = (int64_t)m.page[s] * p.block_size + t0 % p.block_size;
+  const int row = p.hkv * HD;  // elements (bf16) or bytes (E4M3FN) between tokens
+  const int64_t base = slot0 * row + (int64_t)m.h * HD;
   if constexpr (!FP8) {
     const uint16_t* kc = static_cast<const uint16_t*>(p.k_cache) + base;
     const uint16_t* vc = static_cast<const uint16_t*>(p.v_cache) + base;
@@ -547,12 +554,12 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(kc + r * row + sw * 8 * (n ^ (r & 15)), dst + i * 1024);
+      dma16(kc + r * row + 8 * (n ^ (r & 15)), dst + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(vc + r * row + sw * 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
+      dma16(vc + r * row + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
     }
   } else {
     const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
@@ -561,17 +568,17 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(kc + r * row + sw * 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
+      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(vc + r * row + sw * 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
+      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
     }
     // Lanes 0-15: K scales of the 16 tokens, lanes 16-31: V scales (lanes
     // 32-63 repeat them into unused bytes).
     const float* sc = (lane & 16) ? p.v_scale : p.k_scale;
-    dma4(sc + (live ? (slot0 + (lane & 15)) * p.hkv + m.h : 0), dst + 4096);
+    dma4(sc + (slot0 + (lane & 15)) * p.hkv + m.h, dst + 4096);
   }
 }
 
@@ -658,7 +665,9 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
   for (int i = 0; i < 4; ++i) {
     e[i] = __builtin_amdgcn_exp2f(x[i] - mu);
     rs += e[i];
-    if constexpr (FP8) e[i] *= vsc[i];
+    // Scales of tokens past the valid ones are whatever the pool (or LDS)
+    // holds there: such a token's probability is 0 whatever its scale.
+    if constexpr (FP8) e[i] = 4 * g + i < ntok ? e[i] * vsc[i] : 0.0f;
   }
   rs = col_sum(rs);
   l = l * alpha + rs;
