@@ -861,12 +861,14 @@ __device__ __forceinline__ void wait_vm(int extra) {
 //
 // Vector memory operations of item k (cur), in issue order; G = step loads per
 // wavefront, H = merge stores per wavefront, [0] = wavefront 0 only:
-//   step 0: [0] fetch (claims the item after nxt)     step (cur, 2)
-//   step 1: [0] ticket of prev   Q(nxt)                step (cur, 3)
-//   step 2: step (nxt, 0)   [0] metadata of the item after nxt
-//   step 3: merge stores (H)   step (nxt, 1)
-// so the waits before steps 0..3 allow H+G+[1], G+[1], G+1+[1], G+[1] younger
-// operations.
+//   step 0: step (cur, 2)
+//   step 1: [0] ticket of prev   [0] metadata of nxt   step (cur, 3)
+//   step 2: Q(nxt)   step (nxt, 0)
+//   step 3: merge stores (H)   step (nxt, 1)   [0] fetch of the item after nxt
+// so the waits before steps 0..3 allow H+G+[1], G, G, G+1 younger operations.
+// nxt is learned at step 1 from the fetch issued at the end of the previous
+// item, so a workgroup holds at most its current item and one claimed item
+// that has not started.
 template <bool FP8>
 __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
                            uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
@@ -875,37 +877,28 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   const int n = lane & 15, g = lane >> 4;
   const bool w0 = wave == 0;
   const bool half = dchunk < CHUNK;  // steps 2 and 3 of every item are empty
-  const int x0 = w0 ? 1 : 0;
   uint8_t* sa = st0 + wave * WSTAGE;  // even steps
   uint8_t* sb = st1 + wave * WSTAGE;  // odd steps
   constexpr int GROUP = d_group<FP8>();
   const int hgp = (p.G + 3) >> 2;  // merge stores per wavefront and item
   auto item_of = [&](uint32_t rel) { return decode_base + list + (int)rel * nlist; };
 
-  // Prologue: the first item's metadata and the fetch of the item after it,
-  // then the same operations the loop's last step leaves in flight.
+  // Prologue: the first item's metadata, then the same operations the
+  // loop's last step leaves in flight (with stand-in stores for the merge).
   DMeta cur = decode_geom(p, r0, __builtin_amdgcn_readfirstlane(item_of(rel0) - sm.off[r0]), item_of(rel0), decode_base,
                           dchunk);
-  uint32_t f = 0;
-  if (tid == 0) f = atomic_add_ret(ctr, 1u);
   if (w0) decode_meta_dma(p, sm, cur, 0, lane);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  if (tid == 0) sm.item = after_wait(f) - base;
   lds_sync();
   decode_meta_read(cur, sm, 0);
-  bool has1 = __builtin_amdgcn_readfirstlane(sm.item) < count;  // nxt exists
-  DMeta nxt = cur;
-  if (has1) {
-    const int item = item_of(__builtin_amdgcn_readfirstlane(sm.item));
-    const int r = find_row(sm, item, p.np, nrows, lane);
-    nxt = decode_geom(p, r, __builtin_amdgcn_readfirstlane(item - sm.off[r]), item, decode_base, dchunk);
-  }
   decode_issue_q(p, qbuf, cur, wave, lane);
   decode_issue<FP8>(p, sa, cur, 0, wave, lane);
-  if (w0) decode_meta_dma(p, sm, nxt, 1, lane);
   for (int i = 0; i < hgp; ++i)
     if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
   decode_issue<FP8>(p, sb, cur, 1, wave, lane);
+  uint32_t f = 0;
+  bool fetching = true;  // the fetch in flight is a real one
+  if (tid == 0) f = atomic_add_ret(ctr, 1u);
 
   DMeta prev = cur;
   bool due = false;  // prev's partial is stored and its ticket not yet taken
@@ -914,7 +907,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     uint8_t* qnxt = qbuf + ((k + 1) & 1) * QBUF;
 
     // Step 0: (cur, 0) and Q(cur) have landed.
-    wait_vm<GROUP>(hgp + x0);
+    wait_vm<GROUP>(hgp + (w0 ? 1 : 0));
     lds_sync();
     u32x4 qv[4];
     {
@@ -922,7 +915,6 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qcur + hn * ROWB + 16 * (4 * kk + g));
     }
-    if (tid == 0) f = atomic_add_ret(ctr, has1 ? 1u : 0u);
     f32x4 o[8];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
@@ -931,60 +923,66 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     decode_issue<FP8>(p, sa, cur, 2, wave, lane);
 
     // Step 1: (cur, 1) has landed, and with it prev's stores (every
-    // wavefront's, after the barrier) and nxt's metadata.
-    wait_vm<GROUP>(x0);
+    // wavefront's, after the barrier) and the fetch.  Wavefront 0 finds the
+    // fetched item's row, broadcasts it and loads the item's metadata.
+    wait_vm<GROUP>(0);
     lds_sync();
-    if (has1) decode_meta_read(nxt, sm, (k + 1) & 1);
     if (tid == 0) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], due ? 1u : 0u);
     due = false;
-    decode_issue_q(p, qnxt, nxt, wave, lane);
+    bool has1 = false;
+    DMeta nxt = cur;
+    if (w0) {
+      if (fetching) {
+        const uint32_t rel1 = __builtin_amdgcn_readfirstlane(after_wait(f)) - base;
+        has1 = rel1 < count;
+        if (has1) {
+          const int item = item_of(rel1);
+          const int r = find_row(sm, item, p.np, nrows, lane);
+          const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
+          nxt = decode_geom(p, r, local, item, decode_base, dchunk);
+          if (tid == 0) {
+            sm.bcast[0] = r;
+            sm.bcast[1] = local;
+          }
+        }
+        if (tid == 0) sm.item = rel1;
+      }
+      decode_meta_dma(p, sm, nxt, (k + 1) & 1, lane);
+    }
     decode_step<FP8>(p, sb, decode_ntok(p, cur, 1, wave), qv, o, m, l, lane);
     decode_issue<FP8>(p, sb, cur, 3, wave, lane);
 
-    // Step 2: (cur, 2) and the fetch have landed.  Wavefront 0 finds the
-    // fetched item's row, broadcasts it and loads the item's metadata.
-    wait_vm<GROUP + 1>(x0);
-    bool has2 = false;
-    DMeta nxt2 = nxt;
-    if (w0 && has1) {
-      const uint32_t rel2 = __builtin_amdgcn_readfirstlane(after_wait(f)) - base;
-      has2 = rel2 < count;
-      if (has2) {
-        const int item = item_of(rel2);
-        const int r = find_row(sm, item, p.np, nrows, lane);
-        const int local = __builtin_amdgcn_readfirstlane(item - sm.off[r]);
-        nxt2 = decode_geom(p, r, local, item, decode_base, dchunk);
-        if (tid == 0) {
-          sm.bcast[0] = r;
-          sm.bcast[1] = local;
-        }
+    // Step 2: (cur, 2) and nxt's metadata have landed; the broadcast is
+    // visible after the barrier.
+    wait_vm<GROUP>(0);
+    lds_sync();
+    if (fetching) {
+      const uint32_t rel1 = __builtin_amdgcn_readfirstlane(sm.item);
+      has1 = rel1 < count;
+      if (has1) {
+        if (!w0)
+          nxt = decode_geom(p, __builtin_amdgcn_readfirstlane(sm.bcast[0]),
+                            __builtin_amdgcn_readfirstlane(sm.bcast[1]), item_of(rel1), decode_base, dchunk);
+        decode_meta_read(nxt, sm, (k + 1) & 1);
       }
-      if (tid == 0) sm.item = rel2;
     }
+    if (!has1) nxt = cur;  // no next item: its loads repeat the current item's
+    decode_issue_q(p, qnxt, nxt, wave, lane);
     if (!half) decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
     decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
-    if (w0) decode_meta_dma(p, sm, has2 ? nxt2 : nxt, k & 1, lane);
 
-    // Step 3: (cur, 3) has landed; the broadcast is visible after the barrier.
-    wait_vm<GROUP>(x0);
-    lds_sync();
-    if (has1 && !w0) {
-      const uint32_t rel2 = __builtin_amdgcn_readfirstlane(sm.item);
-      has2 = rel2 < count;
-      if (has2)
-        nxt2 = decode_geom(p, __builtin_amdgcn_readfirstlane(sm.bcast[0]), __builtin_amdgcn_readfirstlane(sm.bcast[1]),
-                           item_of(rel2), decode_base, dchunk);
-    }
+    // Step 3: (cur, 3) has landed.
+    wait_vm<GROUP + 1>(0);
     if (!half) decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
     decode_issue<FP8>(p, sb, nxt, 1, wave, lane);
+    fetching = fetching && has1;
+    if (tid == 0) f = atomic_add_ret(ctr, fetching ? 1u : 0u);
     prev = cur;
     due = decode_nch(p, cur) > 1;
     if (!has1) break;
     cur = nxt;
-    if (has2) nxt = nxt2;
-    has1 = has2;
   }
   // The last item's stores (and the repeated loads) complete here.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
