@@ -1375,21 +1375,41 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // b + grid/2 share a CU and each CU pairs an MFMA-bound prefill workgroup
   // with an HBM-bound decode one.
   const int first = 2 * (int)blockIdx.x >= (int)gridDim.x ? 1 : 0;
+  // Static first items: the workgroups of a list that start with a family
+  // (all of them when the list has items in one family only) take that
+  // family's first items by their index, without a fetch; fetched relative
+  // indices start after them (S of them), a family is fetched count - S + wgs
+  // times per launch (one out-of-list fetch per workgroup), and the last
+  // fetcher advances the base by that much.
+  const int member = blockIdx.x / nlist;  // index of this workgroup in its list
+  const int half_grid = gridDim.x / 2;
+  const int wfirst0 = half_grid > list ? (half_grid - list + nlist - 1) / nlist : 0;  // prefill-first members
+  uint32_t fcount[2];
+#pragma unroll
+  for (int fam = 0; fam < 2; ++fam) {
+    const int fsize = fam ? total - decode_base : decode_base;
+    fcount[fam] = list < fsize ? (uint32_t)((fsize - list + nlist - 1) / nlist) : 0u;
+  }
+  const bool both = fcount[0] > 0 && fcount[1] > 0;
   if (tid == 0) sm.salt = 0;
   for (int pass = 0; pass < 2; ++pass) {
     const int fam = first ^ pass;
     const int fbase = fam ? decode_base : 0;
-    const int fsize = fam ? total - decode_base : decode_base;
-    const uint32_t count = list < fsize ? (uint32_t)((fsize - list + nlist - 1) / nlist) : 0u;
+    const uint32_t count = fcount[fam];
     // A list without items this launch is not touched: its base stays valid.
     if (count == 0) continue;
+    const int wfam = both ? (fam ? (int)wgs - wfirst0 : wfirst0) : (int)wgs;  // members starting here
+    const int jfam = both ? (fam ? member - wfirst0 : member) : member;      // this one's index among them
+    const bool starts_here = !both || fam == first;
+    const uint32_t S = min(count, (uint32_t)wfam);  // static items of this family
+    const bool has_static = starts_here && jfam >= 0 && (uint32_t)jfam < count;
     uint32_t* ctr = reinterpret_cast<uint32_t*>(p.ctrl) + (fam * NLIST + list) * CTRL_STRIDE;
     if (tid == 0) {
-      sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm.item = atomicAdd(ctr, 1u) - sm.base;  // relative fetch index
+      sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - S;
+      sm.item = has_static ? (uint32_t)jfam : atomicAdd(ctr, 1u) - sm.base;  // relative index
     }
     __syncthreads();
-    const uint32_t base = sm.base;
+    const uint32_t base = sm.base;  // counter value of relative index 0 (before the static ones)
 
     // Publishes the fetched-ahead index to the workgroup and returns it.
     auto advance = [&](uint32_t next) -> uint32_t {
