@@ -677,13 +677,23 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
     for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
   }
   // P^T as the B operand of the 16x16x16 product: k slot (g, j) is token 4g + j.
-  const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])});
+  // P goes in as two bf16 terms, hi = bf16(e) and lo = bf16(e - hi) (the
+  // difference is exact in fp32), so the product carries P to about 2^-17
+  // relative instead of bf16's 2^-9.  The stream is HBM-bound; the second
+  // product costs MFMA cycles that are idle anyway.
+  const uint32_t h01 = pack_bf16x2(e[0], e[1]), h23 = pack_bf16x2(e[2], e[3]);
+  const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{h01, h23});
+  const s16x4 pl = __builtin_bit_cast(s16x4, u32x2{
+      pack_bf16x2(e[0] - __uint_as_float(h01 << 16), e[1] - __uint_as_float(h01 & 0xffff0000u)),
+      pack_bf16x2(e[2] - __uint_as_float(h23 << 16), e[3] - __uint_as_float(h23 & 0xffff0000u))});
   if constexpr (FP8) {  // the decoded tile is read only now
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
   }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt], 0, 0, 0);
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pl, o[dt], 0, 0, 0);
 }
 
 // Cross-wavefront merge.  Per pass of 4 query heads, every wavefront writes
