@@ -10,10 +10,11 @@
 // belongs to list i % 8 and workgroup b serves list b % 8; the prefill items
 // and the decode items of a list form two families, and workgroups start with
 // one family or the other alternately so both phases begin at once.  Each list
-// has a monotonic fetch counter and a base word on its own 128-byte line: the
-// workgroup that makes a family's last fetch advances its base, so counters
-// never need a reset or memset.  The grid is sized from capacities, never from
-// device data, so the launch can be recorded in a HIP graph.
+// has a fetch counter on its own 128-byte line that is zero between launches:
+// a launch makes a known number of fetches on it, and the workgroup that makes
+// the last one resets it, so no memset is needed.  The grid is sized from
+// capacities, never from device data, so the launch can be recorded in a HIP
+// graph.
 //
 //  * Prefill item (row r, block of 16 or 32 query positions, kv head h): each
 //    wavefront owns one of the G query heads that share kv head h, for the
@@ -125,7 +126,7 @@ struct Params {
   int32_t G;
   int32_t HG;  // ceil(G / 4): wavefront groups per kv head in prefill
   float scale_log2;
-  int* ctrl;      // per list: [0] fetch counter, [1] base of the current launch
+  int* ctrl;      // per list: [0] fetch counter (zero between launches)
   int* counters;  // split-K tickets, [num_decode * hkv]
   float* partials;
 };
@@ -154,7 +155,6 @@ struct Smem {
   int wmax[4];
   int dsum[4];
   uint32_t item;
-  uint32_t base;
   int row;
   int salt;
   int meta[2][8];   // decode: landed row length and block-table entries, by item parity
@@ -330,15 +330,6 @@ __device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& 
   tmax = (min(g.Lk, max(0, g.prefix + g.Lq)) + TT - 1) / TT;
   const int mean = (min(g.Lk, max(0, g.prefix + (g.Lq + 1) / 2)) + TT - 1) / TT;
   work = nqb * max(mean, 1) * p.hkv * p.HG;
-}
-
-__device__ __forceinline__ int row_items(const Params& p, int r, int bq, int dchunk) {
-  if (r < p.np) {
-    const int lq = p.cu_q[r + 1] - p.cu_q[r];
-    return lq > 0 ? ((lq + bq - 1) / bq) * p.hkv * p.HG : 0;
-  }
-  const int L = decode_len(p, r - p.np);
-  return max(1, (L + dchunk - 1) / dchunk) * p.hkv;
 }
 
 __device__ __forceinline__ void store_partial(float* p, float v) {
@@ -806,24 +797,20 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // chunk increments the ticket only after its partial stores are complete, and
 // the chunks are processed by running workgroups that never wait on merge
 // tasks), merges, and resets the ticket for the next launch.  Like the work
-// lists, a counter only grows: a launch makes exactly tasks + workgroups
-// fetches on it, and the workgroup making the last one advances its base.
+// lists, a counter starts at zero: a launch makes exactly tasks + workgroups
+// fetches on it, and the workgroup making the last one resets it.
 __device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
   uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (2 * NLIST + list) * CTRL_STRIDE;
   const int ntask = p.nd * p.hkv;
   const uint32_t count = list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u;
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
-  if (tid == 0) sm.base = __hip_atomic_load(mctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  lds_sync();
-  const uint32_t base = sm.base;
   for (;;) {
-    if (tid == 0) sm.item = atomicAdd(mctr, 1u) - base;
+    if (tid == 0) sm.item = atomicAdd(mctr, 1u);
     lds_sync();
     const uint32_t rel = __builtin_amdgcn_readfirstlane(sm.item);
     lds_sync();
     if (rel >= count) {
-      if (tid == 0 && rel == count + wgs - 1u)
-        __hip_atomic_store(mctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && rel == count + wgs - 1u) __hip_atomic_store(mctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     const int task = list + (int)rel * nlist;
@@ -1291,8 +1278,11 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
-  const int per = (nrows + NT - 1) / NT;
+  const int per = (nrows + NT - 1) / NT;  // rows per thread, at most 4
   const int r0 = tid * per;
+  const int nlist = min((int)gridDim.x, NLIST);
+  const int list = blockIdx.x % nlist;
+
 
   // Prefill block size: a launch with decode rows uses 32 query positions
   // (the decode work hides the longest prefill item and 32 halves the key
@@ -1303,18 +1293,33 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // else CHUNK_MIN (short launches need the parallelism more than the longer
   // items' lower per-token overhead).
   int bq = 32, dchunk = CHUNK;
+  // Item counts of this thread's rows under either choice (32-position
+  // blocks / CHUNK, 16-position blocks / CHUNK_MIN), so the metadata is read
+  // once.
+  int cnt_a[4], cnt_b[4];
   {
     int w = 0, tm = 0, dn = 0;
-    for (int r = r0; r < min(r0 + per, nrows); ++r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + i;
+      cnt_a[i] = cnt_b[i] = 0;
+      if (i >= per || r >= nrows) continue;
       if (r < p.np) {
         int wr, tr;
         pf_work(p, r, wr, tr);
         w += wr;
         tm = max(tm, tr);
+        const int lq = p.cu_q[r + 1] - p.cu_q[r];
+        cnt_a[i] = lq > 0 ? ((lq + 31) / 32) * p.hkv * p.HG : 0;
+        cnt_b[i] = lq > 0 ? ((lq + 15) / 16) * p.hkv * p.HG : 0;
       } else {
-        dn += (decode_len(p, r - p.np) + CHUNK - 1) / CHUNK;
+        const int L = decode_len(p, r - p.np);
+        dn += (L + CHUNK - 1) / CHUNK;
+        cnt_a[i] = max(1, (L + CHUNK - 1) / CHUNK) * p.hkv;
+        cnt_b[i] = max(1, (L + CHUNK_MIN - 1) / CHUNK_MIN) * p.hkv;
       }
     }
+
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       w += __shfl_xor(w, d, 64);
@@ -1341,8 +1346,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   }
 
   // Per-row item counts -> exclusive prefix in sm.off (block-wide scan).
+  int cnt[4];
   int local_sum = 0;
-  for (int r = r0; r < min(r0 + per, nrows); ++r) local_sum += row_items(p, r, bq, dchunk);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool alt = r0 + i < p.np ? bq == 16 : dchunk == CHUNK_MIN;
+    cnt[i] = alt ? cnt_b[i] : cnt_a[i];
+    local_sum += cnt[i];
+  }
   int incl = local_sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -1353,9 +1364,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   __syncthreads();
   int run = incl - local_sum;
   for (int w = 0; w < wave; ++w) run += sm.wsum[w];
-  for (int r = r0; r < min(r0 + per, nrows); ++r) {
-    sm.off[r] = run;
-    run += row_items(p, r, bq, dchunk);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < per && r0 + i < nrows) sm.off[r0 + i] = run;
+    run += cnt[i];
   }
   if (tid == NT - 1) sm.off[nrows] = run;
   __syncthreads();
@@ -1370,14 +1382,13 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // L2).  Workgroups of a list start with different families and take the
   // other one when theirs is exhausted, so MFMA-bound prefill items
   // and HBM-bound decode items run side by side from the start.  A list's
-  // counter only grows; the list's base is the counter value at which this
-  // launch's items start.  Every workgroup reads the base before its first
-  // fetch and stops after its first fetch past the list, so a launch makes
-  // exactly count + workgroups fetches on a list and the workgroup that makes
-  // the last one advances the base for the next launch.  No counter is ever
-  // reset or contended by a completion count.
-  const int nlist = min((int)gridDim.x, NLIST);
-  const int list = blockIdx.x % nlist;
+  // counter is zero when a launch starts.  Every workgroup stops after its
+  // first fetch past the list, so a launch makes exactly count + workgroups
+  // fetches on a list (fewer by the static first items below), and the
+  // workgroup that makes the last one (the one returning the largest value)
+  // resets the counter: every other workgroup has made its last fetch by
+  // then.  Fetches that add 0 (decode loop padding) may follow the reset;
+  // their results are ignored.  No counter is contended by a completion count.
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
   // Family taken first (0 prefill, 1 decode): the first half of the grid
   // starts with prefill, the second with decode.  The dispatcher fills every
@@ -1388,9 +1399,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // Static first items: the workgroups of a list that start with a family
   // (all of them when the list has items in one family only) take that
   // family's first items by their index, without a fetch; fetched relative
-  // indices start after them (S of them), a family is fetched count - S + wgs
-  // times per launch (one out-of-list fetch per workgroup), and the last
-  // fetcher advances the base by that much.
+  // indices start after them (fetch value f is relative index S + f), and a
+  // family is fetched count - S + wgs times per launch (one out-of-list fetch
+  // per workgroup).
   const int member = blockIdx.x / nlist;  // index of this workgroup in its list
   const int half_grid = gridDim.x / 2;
   const int wfirst0 = half_grid > list ? (half_grid - list + nlist - 1) / nlist : 0;  // prefill-first members
@@ -1406,7 +1417,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     const int fam = first ^ pass;
     const int fbase = fam ? decode_base : 0;
     const uint32_t count = fcount[fam];
-    // A list without items this launch is not touched: its base stays valid.
+    // A list without items this launch is not touched: its counter stays zero.
     if (count == 0) continue;
     const int wfam = both ? (fam ? (int)wgs - wfirst0 : wfirst0) : (int)wgs;  // members starting here
     const int jfam = both ? (fam ? member - wfirst0 : member) : member;      // this one's index among them
@@ -1414,12 +1425,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     const uint32_t S = min(count, (uint32_t)wfam);  // static items of this family
     const bool has_static = starts_here && jfam >= 0 && (uint32_t)jfam < count;
     uint32_t* ctr = reinterpret_cast<uint32_t*>(p.ctrl) + (fam * NLIST + list) * CTRL_STRIDE;
-    if (tid == 0) {
-      sm.base = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - S;
-      sm.item = has_static ? (uint32_t)jfam : atomicAdd(ctr, 1u) - sm.base;  // relative index
-    }
+    const uint32_t base = 0u - S;  // fetch value of relative index 0: relative = fetch value + S
+    if (tid == 0) sm.item = has_static ? (uint32_t)jfam : atomicAdd(ctr, 1u) - base;  // relative index
     __syncthreads();
-    const uint32_t base = sm.base;  // counter value of relative index 0 (before the static ones)
 
     // Publishes the fetched-ahead index to the workgroup and returns it.
     auto advance = [&](uint32_t next) -> uint32_t {
@@ -1469,8 +1477,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
                         dchunk, ltid);
       break;
     }
-    if (tid == 0 && sm.item == count + wgs - 1u)
-      __hip_atomic_store(ctr + 1, base + count + wgs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0 && sm.item == count + wgs - 1u) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
   if constexpr (HAS_DEC) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
