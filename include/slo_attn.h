@@ -66,6 +66,35 @@ int slo_store_kvcache(const void* key, int64_t key_row_stride,
                       int64_t num_slots, float scale_floor, slo_stream_t stream);
 
 /*
+ * Fused q/k RMSNorm, rotary embedding and KV-cache write, one pass over the
+ * fused QKV projection output.
+ *
+ * Replaces the steps between qkv_proj and the attention call in
+ * Qwen3Attention.forward (nanovllm/models/qwen3.py:80-86): q_norm and k_norm
+ * (RMSNorm over head_dim, nanovllm/layers/layernorm.py:16-26), rotary_emb
+ * (nanovllm/layers/rotary_embedding.py:6-14,37-48) and the store_kvcache that
+ * Attention.forward issues before attending (nanovllm/layers/attention.py:
+ * 10-40,59-66).  Row i of `qkv` holds num_heads q heads, then num_kv_heads k
+ * heads, then num_kv_heads v heads of head_dim bf16 each (rows
+ * `qkv_row_stride` elements apart).  Writes q_out [num_tokens, num_heads,
+ * head_dim] and k_out [num_tokens, num_kv_heads, head_dim] (bf16, contiguous;
+ * q and k normalised and rotated), and, for tokens whose slot is not -1, the
+ * rotated k and the unchanged v into the pool exactly as slo_store_kvcache
+ * does (E4M3FN with scales when kv_dtype says so).  positions are int64;
+ * cos_sin is the fp32 [max_position, head_dim] table whose row p is
+ * cos(p*inv_freq) then sin(p*inv_freq) (the reference's cos_sin_cache);
+ * positions outside [0, max_position) are clamped into it.  q/k norm weights
+ * are bf16 [head_dim].  head_dim must be 128.
+ */
+int slo_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,
+                           int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                           int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight,
+                           float eps, const float* cos_sin, int32_t max_position, void* q_out,
+                           void* k_out, const int32_t* slot_mapping, int32_t kv_dtype,
+                           void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                           int64_t num_slots, float scale_floor, slo_stream_t stream);
+
+/*
  * Arguments of one ragged paged-attention launch.  Query rows [0, num_decode)
  * are decode rows (one query each, attending to decode_lens[b] cached tokens
  * through decode_tables[b]); query rows num_decode + [cu_q[r], cu_q[r+1]) are

@@ -70,4 +70,29 @@ __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }
 
+// E4M3FN codes of this lane's 8 values of one (token, kv head) vector held by
+// GROUP adjacent lanes (the quantisation contract of
+// docs/project_manual.md:527-537): amax over the vector (cross-lane), scale =
+// amax == 0 ? 1 : max(amax / 448, scale_floor) (correctly rounded division),
+// code = E4M3FN_RNE(clamp(x / scale, -448, 448)).  Returns the 8 code bytes
+// and the scale.
+template <int GROUP>
+__device__ __forceinline__ u32x2 e4m3_encode8(const float (&f)[8], float scale_floor, float& scale) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+#pragma unroll
+  for (int mask = 1; mask < GROUP; mask <<= 1) amax = wave_max_xor(amax, mask);
+  scale = amax == 0.0f ? 1.0f : fmaxf(amax / kFp8Max, scale_floor);
+  float y[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = fminf(fmaxf(f[j] / scale, -kFp8Max), kFp8Max);
+  uint32_t w0 = 0, w1 = 0;
+  w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], w0, false);
+  w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w0, true);
+  w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], w1, false);
+  w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], w1, true);
+  return u32x2{w0, w1};
+}
+
 }  // namespace slo

@@ -41,25 +41,9 @@ store_kvcache_kernel(const uint16_t* __restrict__ key, int64_t key_stride,
         f[2 * j] = bf16_bits_to_f32(x[j] & 0xffffu);
         f[2 * j + 1] = bf16_bits_to_f32(x[j] >> 16);
       }
-      float amax = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
-#pragma unroll
-      for (int mask = 1; mask < CPH; mask <<= 1) amax = wave_max_xor(amax, mask);
-      // Correctly rounded fp32 division, as the CPU definition requires.
-      const float scale = amax == 0.0f ? 1.0f : fmaxf(amax / kFp8Max, scale_floor);
-      uint32_t w0 = 0, w1 = 0;
-      float y[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = fminf(fmaxf(f[j] / scale, -kFp8Max), kFp8Max);
-      w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], w0, false);
-      w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w0, true);
-      w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], w1, false);
-      w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], w1, true);
+      float scale;
+      const u32x2 packed = e4m3_encode8<CPH>(f, scale_floor, scale);
       uint8_t* cache = static_cast<uint8_t*>(is_v ? v_cache : k_cache);
-      u32x2 packed;
-      packed.x = w0;
-      packed.y = w1;
       *reinterpret_cast<u32x2*>(cache + dst) = packed;
       if ((cc % CPH) == 0) (is_v ? v_scale : k_scale)[slot * num_kv_heads + cc / CPH] = scale;
     }

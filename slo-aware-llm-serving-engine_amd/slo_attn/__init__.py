@@ -8,11 +8,12 @@ ragged mixed prefill/decode paged-attention launch, exposed through the same
 """
 from .context import Context, get_context, reset_context, set_context
 from .mixed_attention import MixedAttentionContext, forward_mixed
-from .ops import paged_attention, reserve_workspace, store_kvcache
+from .ops import paged_attention, qk_norm_rope_store, reserve_workspace, rope_cos_sin, store_kvcache
 from .attention import Attention
 from . import _lib
 
 __all__ = [
     "Attention", "Context", "MixedAttentionContext", "forward_mixed", "get_context",
-    "paged_attention", "reserve_workspace", "reset_context", "set_context", "store_kvcache",
+    "paged_attention", "qk_norm_rope_store", "reserve_workspace", "reset_context", "rope_cos_sin",
+    "set_context", "store_kvcache",
 ]

@@ -13,6 +13,8 @@ Mirrors nanovllm/layers/attention.py:33-79: same constructor, attributes
 Optional ``k_scale`` / ``v_scale`` attributes (fp32
 ``[num_blocks, block_size, num_kv_heads]``) select the E4M3FN pool when the
 runner assigns uint8 / float8_e4m3fn ``k_cache`` / ``v_cache`` views.
+``forward(q, k, v, kv_stored=True)`` skips the KV write, for callers whose
+``qk_norm_rope_store`` already wrote this step's K/V into the pool.
 """
 from __future__ import annotations
 
@@ -24,6 +26,10 @@ from .mixed_attention import forward_mixed
 from .ops import paged_attention, store_kvcache
 
 __all__ = ["Attention", "store_kvcache"]
+
+
+def _stored(*args):
+    """store_fn for a step whose K/V are already in the pool."""
 
 
 class Attention(nn.Module):
@@ -40,14 +46,14 @@ class Attention(nn.Module):
     def _scales(self):
         return () if self.k_scale is None else (self.k_scale, self.v_scale)
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
         if context.mixed is not None:
-            return forward_mixed(q, k, v, k_cache, v_cache, context, self.scale, store_kvcache,
-                                 self.k_scale, self.v_scale)
+            return forward_mixed(q, k, v, k_cache, v_cache, context, self.scale,
+                                 _stored if kv_stored else store_kvcache, self.k_scale, self.v_scale)
         have_cache = bool(k_cache.numel() and v_cache.numel())
-        if have_cache:
+        if have_cache and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, *self._scales())
         if context.is_prefill:
             rows = context.cu_seqlens_q.numel() - 1

@@ -101,6 +101,81 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         float(scale_floor), _stream(device)), "slo_store_kvcache")
 
 
+# ------------------------------------------- fused q/k norm + RoPE + KV write
+def rope_cos_sin(head_dim: int, max_position: int, base: float, device) -> torch.Tensor:
+    """fp32 [max_position, head_dim] table: cos(p * inv_freq) then sin(p * inv_freq).
+
+    The cos_sin_cache of RotaryEmbedding (nanovllm/layers/rotary_embedding.py:27-35),
+    built with the same torch operations on ``device``.
+    """
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float, device=device) / head_dim))
+    t = torch.arange(max_position, dtype=torch.float, device=device)
+    freqs = torch.einsum("i,j -> ij", t, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).contiguous()
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight: torch.Tensor,
+                       k_norm_weight: torch.Tensor, eps: float, cos_sin: torch.Tensor, num_heads: int,
+                       num_kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor, k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None, head_dim: int = 128,
+                       scale_floor: float = _lib.FP8_SCALE_FLOOR):
+    """q_norm, k_norm, rotary_emb and the KV write of one layer in one launch.
+
+    Covers nanovllm/models/qwen3.py:80-86 up to the attention call, and the
+    store_kvcache that Attention.forward would issue (attention.py:59-66).
+    ``qkv``: ``[N, (num_heads + 2*num_kv_heads) * head_dim]`` bf16 (the fused
+    projection output; rows may be strided).  Returns ``(q, k, v)``: q and k
+    normalised and rotated (new contiguous bf16 tensors), v a view of ``qkv``.
+    The pool receives the rotated k and v at ``slot_mapping`` (bf16 or
+    E4M3FN with ``k_scale``/``v_scale``), as ``store_kvcache`` writes them.
+    """
+    if qkv.dim() != 2 or qkv.stride(-1) != 1:
+        raise ValueError("qkv must be a [tokens, width] tensor with contiguous rows")
+    N = qkv.shape[0]
+    width = (num_heads + 2 * num_kv_heads) * head_dim
+    if qkv.shape[1] != width:
+        raise ValueError(f"qkv rows must hold {width} elements")
+    device = _require_gpu(qkv, positions, q_norm_weight, k_norm_weight, cos_sin, k_cache, v_cache,
+                          slot_mapping, k_scale, v_scale)
+    if qkv.dtype != torch.bfloat16:
+        raise TypeError("qkv must be bf16")
+    if positions.dtype != torch.int64 or positions.numel() != N or not positions.is_contiguous():
+        raise ValueError("positions must be a contiguous int64 [tokens] tensor")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w.dtype != torch.bfloat16 or w.numel() != head_dim or not w.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 [head_dim] tensor")
+    if cos_sin.dtype != torch.float32 or cos_sin.dim() != 2 or cos_sin.shape[1] != head_dim or \
+            not cos_sin.is_contiguous():
+        raise ValueError("cos_sin must be a contiguous fp32 [max_position, head_dim] table")
+    code = kv_dtype_code(k_cache)
+    if kv_dtype_code(v_cache) != code:
+        raise TypeError("k_cache and v_cache formats differ")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV pool views must be contiguous")
+    if k_cache.shape[-2:] != (num_kv_heads, head_dim) or v_cache.shape != k_cache.shape:
+        raise ValueError("KV pool must be [num_blocks, block_size, num_kv_heads, head_dim]")
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
+    if code == _lib.KV_FP8_E4M3FN:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an E4M3FN pool needs k_scale and v_scale")
+        for sc in (k_scale, v_scale):
+            if sc.dtype != torch.float32 or not sc.is_contiguous() or sc.numel() != num_slots * num_kv_heads:
+                raise ValueError("scale pools must be contiguous fp32 [num_blocks, block_size, num_kv_heads]")
+    _int32(slot_mapping, "slot_mapping")
+    if slot_mapping.numel() != N:
+        raise ValueError("slot_mapping must hold one slot per token")
+    q = torch.empty((N, num_heads, head_dim), dtype=torch.bfloat16, device=qkv.device)
+    k = torch.empty((N, num_kv_heads, head_dim), dtype=torch.bfloat16, device=qkv.device)
+    _lib.check(_lib.load().slo_qk_norm_rope_store(
+        _ptr(qkv), qkv.stride(0), _ptr(positions), N, num_heads, num_kv_heads, head_dim, _ptr(q_norm_weight),
+        _ptr(k_norm_weight), float(eps), _ptr(cos_sin), cos_sin.shape[0], _ptr(q), _ptr(k), _ptr(slot_mapping),
+        code, _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), num_slots, float(scale_floor),
+        _stream(device)), "slo_qk_norm_rope_store")
+    v = qkv[:, (num_heads + num_kv_heads) * head_dim:].view(N, num_kv_heads, head_dim)
+    return q, k, v
+
+
 # ---------------------------------------------------------------- workspace
 _ws_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}
