@@ -18,6 +18,8 @@ slot-mapped KV write of the 1048 new tokens + ONE ragged attention launch.
   time the split launches (decode rows only against HBM, prefill rows only
   against bf16 MFMA peak), the mode that mirrors the reference's per-phase
   flash-attn calls.
+* roofline_qk_norm_rope_store: the step before attention (q/k RMSNorm, RoPE
+  and the KV write fused into one launch) on the same new tokens, against HBM.
 * cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
   step.
 """
@@ -60,7 +62,7 @@ def main():
               "(the attention path runs at TP=1 and this build has no multi-GPU path).", file=sys.stderr)
         sys.exit(2)
     import torch
-    from slo_attn import _lib, forward_mixed, reserve_workspace, store_kvcache, workloads
+    from slo_attn import _lib, forward_mixed, qk_norm_rope_store, reserve_workspace, rope_cos_sin, store_kvcache, workloads
     from slo_attn.ops import paged_attention
     from types import SimpleNamespace
 
@@ -188,6 +190,34 @@ def main():
     dec_gbs = (dec_bytes + 2 * w.num_decode * hq * d * 2) / (t_dec * 1e-6) / 1e9
     pre_tflops = flops / (t_pre * 1e-6) / 1e12
 
+    # ---- the step before attention: fused q/k RMSNorm + RoPE + KV write of the
+    # same new tokens from a synthetic QKV projection output [tokens, 48*128]
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(tokens, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(device)
+    positions = [L - 1 for L in w.decode_lens]
+    for n, pfx in zip(w.prefill_q, w.prefill_prefix):
+        positions += list(range(pfx, pfx + n))
+    positions = torch.tensor(positions, dtype=torch.int64, device=device)
+    qn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    kn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    cos_sin = rope_cos_sin(d, 40960, 1e6, device)
+    qk_times = []
+    for i in range(args.events + 3):
+        kc, vc, ks, vs = pools[i % nsets]
+        torch.cuda._sleep(200_000)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        qk_norm_rope_store(qkv, positions, qn_w, kn_w, 1e-6, cos_sin, hq, hkv, kc, vc, slots, ks, vs)
+        e1.record()
+        e1.synchronize()
+        if i >= 3:
+            qk_times.append(e0.elapsed_time(e1) * 1e3)
+    t_qk = statistics.mean(qk_times)
+    # read the QKV row, positions and one cos/sin row per token; write q, k and the K/V pool entries
+    qk_bytes = tokens * ((hq + 2 * hkv) * d * 2 + 8 + d * 4 + 4 + (hq + hkv) * d * 2 + 2 * hkv * (d * elem + scale_b))
+    qk_gbs = qk_bytes / (t_qk * 1e-6) / 1e9
+
     # HBM bytes per fused launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE,
     # calibrated against a 256 MiB copy) for this kernel, kept under profiles/.
     traffic = None
@@ -237,6 +267,12 @@ def main():
             "avg_launch_us": round(t_pre, 2), "median_launch_us": round(t_pre_med, 2),
         },
         "split_step_us": round(t_dec + t_pre, 2),
+        "roofline_qk_norm_rope_store": {
+            "bound": "hbm", "achieved": round(qk_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(qk_gbs / HBM_PEAK_GBS, 4), "kernel": "qk_norm_rope_store_kernel",
+            "algorithmic_bytes_per_launch": qk_bytes, "avg_launch_us": round(t_qk, 2),
+            "tokens": tokens,
+        },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

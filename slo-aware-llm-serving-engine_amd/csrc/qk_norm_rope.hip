@@ -18,49 +18,35 @@
 // K is stored after RoPE (docs/project_manual.md:539); V is stored as given.
 // E4M3FN pools use the quantisation of the store kernel.
 //
-// One 16-lane group per (token, head) of the QKV row; lane j holds elements
-// 8j..8j+7 (one 16-byte load), so a head's statistics are a 16-lane
-// reduction and the RoPE partner of element d (d +- 64) sits in lane j ^ 8.
+// One workgroup per token; a 16-lane group per head of the QKV row, lane j
+// holding elements 8j..8j+7 (one 16-byte load), so a head's statistics are a
+// 16-lane reduction and the RoPE partner of element d (d +- 64) sits in lane
+// j ^ 8.
 #include "common.h"
 #include "capi_internal.h"
 
 namespace slo {
 
 constexpr int QK_HD = 128;
+constexpr int QK_UNITS = 4;  // heads per 16-lane group: rows of up to 64 heads
 
-__device__ __forceinline__ float bf16_round(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
-
-__global__ void __launch_bounds__(256)
-qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const int64_t* __restrict__ positions,
-                          int64_t units, int num_heads, int num_kv_heads, const uint16_t* __restrict__ q_w,
-                          const uint16_t* __restrict__ k_w, float eps, const float* __restrict__ cos_sin,
-                          int max_position, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
-                          const int32_t* __restrict__ slot_mapping, int kv_dtype, void* __restrict__ k_cache,
-                          void* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
-                          int64_t num_slots, float scale_floor) {
+// One (token, head) unit: lane j of the 16-lane group holds elements 8j..8j+7
+// of head hh in x.  Writes q_out, or k_out and the pool, or the pool.
+__device__ __forceinline__ void qk_unit(const u32x4& x, int hh, int j, int64_t tok, int64_t slot, bool store,
+                                        int num_heads, int num_kv_heads, const u32x4& wq, const u32x4& wk,
+                                        float eps, const float (&c)[8], const float (&s)[8], uint16_t* q_out,
+                                        uint16_t* k_out, int kv_dtype, void* k_cache, void* v_cache, float* k_scale,
+                                        float* v_scale, float scale_floor) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const int j = lane & 15;
-  const int64_t u = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (u >= units) return;  // whole 16-lane groups leave together
-  const int heads = num_heads + 2 * num_kv_heads;
-  const int64_t tok = u / heads;
-  const int hh = (int)(u % heads);
   const bool is_q = hh < num_heads, is_k = !is_q && hh < num_heads + num_kv_heads;
   const int d0 = 8 * j;
-
-  const u32x4 x = *reinterpret_cast<const u32x4*>(qkv + tok * qkv_stride + (int64_t)hh * QK_HD + d0);
   float f[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     f[2 * i] = bf16_bits_to_f32(x[i] & 0xffffu);
     f[2 * i + 1] = bf16_bits_to_f32(x[i] >> 16);
   }
-
-  const int64_t slot = slot_mapping[tok];
-  const bool store = slot >= 0 && slot < num_slots;
   const int kvh = is_k ? hh - num_heads : hh - num_heads - num_kv_heads;
-
   if (is_q || is_k) {
     // Sum of squares in fp64: every square of a bf16 value is exact and so,
     // for vectors spanning less than 2^15 in magnitude, is the sum, so the
@@ -72,42 +58,40 @@ qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, 
     for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
     const float var = (float)(ss / QK_HD);
     const float r = (float)(1.0 / sqrt((double)(var + eps)));
-    const uint16_t* w = is_q ? q_w : k_w;
-    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + d0);
+    const u32x4 wv = is_q ? wq : wk;
+    // bf16 roundings by v_cvt_pk_bf16_f32 (round to nearest even), two values each.
     float n[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      n[2 * i] = bf16_round(bf16_round(f[2 * i] * r) * bf16_bits_to_f32(wv[i] & 0xffffu));
-      n[2 * i + 1] = bf16_round(bf16_round(f[2 * i + 1] * r) * bf16_bits_to_f32(wv[i] >> 16));
+      const uint32_t a = pack_bf16x2(f[2 * i] * r, f[2 * i + 1] * r);
+      const uint32_t b = pack_bf16x2(__uint_as_float(a << 16) * bf16_bits_to_f32(wv[i] & 0xffffu),
+                                     __uint_as_float(a & 0xffff0000u) * bf16_bits_to_f32(wv[i] >> 16));
+      n[2 * i] = __uint_as_float(b << 16);
+      n[2 * i + 1] = __uint_as_float(b & 0xffff0000u);
     }
-    int64_t pos = positions[tok];
-    pos = pos < 0 ? 0 : (pos >= max_position ? max_position - 1 : pos);
-    const float* cs = cos_sin + pos * QK_HD + (d0 & 63);
-    const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs), c1 = *reinterpret_cast<const f32x4*>(cs + 4);
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(cs + 64), s1 = *reinterpret_cast<const f32x4*>(cs + 68);
-    const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-    const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
     float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float other = __shfl_xor(n[i], 8, 64);  // element d +- 64
+      // element d +- 64: lane j ^ 8 of the 16-lane row (DPP row rotate by 8)
+      const float other = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(n[i]), 0x128, 0xf, 0xf, false));
       const float a = n[i] * c[i], b = other * s[i];
-      y[i] = bf16_round(j < 8 ? a - b : a + b);     // lanes 0-7: x1 half, lanes 8-15: x2 half
+      y[i] = j < 8 ? a - b : a + b;  // lanes 0-7: x1 half, lanes 8-15: x2 half
     }
     u32x4 o;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (__float_as_uint(y[2 * i]) >> 16) | (__float_as_uint(y[2 * i + 1]) & 0xffff0000u);
+    for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
     if (is_q) {
       *reinterpret_cast<u32x4*>(q_out + (tok * num_heads + hh) * QK_HD + d0) = o;
       return;
     }
     *reinterpret_cast<u32x4*>(k_out + (tok * num_kv_heads + kvh) * QK_HD + d0) = o;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = y[i];
-    if (!store) return;
-  } else if (!store) {
-    return;
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(o[i] << 16);
+      f[2 * i + 1] = __uint_as_float(o[i] & 0xffff0000u);
+    }
   }
+  if (!store) return;
   // K (normalised and rotated) or V (as given) into the pool.
   const int64_t dst = (slot * num_kv_heads + kvh) * QK_HD + d0;
   if (kv_dtype == KV_BF16) {
@@ -120,6 +104,49 @@ qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, 
     const u32x2 codes = e4m3_encode8<16>(f, scale_floor, scale);
     *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(is_k ? k_cache : v_cache) + dst) = codes;
     if (j == 0) (is_k ? k_scale : v_scale)[slot * num_kv_heads + kvh] = scale;
+  }
+}
+
+// One workgroup per token: 16-lane group g takes heads g, g+16, g+32, g+48 of
+// the row (all loads first, so a wavefront keeps several in flight).
+__global__ void __launch_bounds__(256)
+qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const int64_t* __restrict__ positions,
+                          int num_heads, int num_kv_heads, const uint16_t* __restrict__ q_w,
+                          const uint16_t* __restrict__ k_w, float eps, const float* __restrict__ cos_sin,
+                          int max_position, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
+                          const int32_t* __restrict__ slot_mapping, int kv_dtype, void* __restrict__ k_cache,
+                          void* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
+                          int64_t num_slots, float scale_floor) {
+  const int j = threadIdx.x & 15;
+  const int grp = threadIdx.x >> 4;
+  const int64_t tok = blockIdx.x;
+  const int heads = num_heads + 2 * num_kv_heads;
+  // Loads in dependency order: the position first (its table row is the only
+  // dependent load), then the row's heads and the norm weights.
+  int64_t pos = positions[tok];
+  const int64_t slot = slot_mapping[tok];
+  const uint16_t* row = qkv + tok * qkv_stride + 8 * j;
+  u32x4 x[QK_UNITS];
+#pragma unroll
+  for (int it = 0; it < QK_UNITS; ++it) {
+    const int hh = grp + 16 * it;
+    x[it] = hh < heads ? *reinterpret_cast<const u32x4*>(row + (int64_t)hh * QK_HD) : u32x4{0, 0, 0, 0};
+  }
+  const u32x4 wq = *reinterpret_cast<const u32x4*>(q_w + 8 * j);
+  const u32x4 wk = *reinterpret_cast<const u32x4*>(k_w + 8 * j);
+  pos = pos < 0 ? 0 : (pos >= max_position ? max_position - 1 : pos);
+  const float* cs = cos_sin + pos * QK_HD + ((8 * j) & 63);
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs), c1 = *reinterpret_cast<const f32x4*>(cs + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(cs + 64), s1 = *reinterpret_cast<const f32x4*>(cs + 68);
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  const bool store = slot >= 0 && slot < num_slots;
+#pragma unroll
+  for (int it = 0; it < QK_UNITS; ++it) {
+    const int hh = grp + 16 * it;
+    if (hh < heads)
+      qk_unit(x[it], hh, j, tok, slot, store, num_heads, num_kv_heads, wq, wk, eps, c, s, q_out, k_out, kv_dtype,
+              k_cache, v_cache, k_scale, v_scale, scale_floor);
   }
 }
 
@@ -154,11 +181,9 @@ extern "C" int slo_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, c
       (reinterpret_cast<uintptr_t>(v_cache) % 16) || (reinterpret_cast<uintptr_t>(cos_sin) % 16) ||
       (reinterpret_cast<uintptr_t>(q_norm_weight) % 16) || (reinterpret_cast<uintptr_t>(k_norm_weight) % 16))
     return fail(SLO_ERR_INVALID, "qk_norm_rope_store: rows and tables must be 16-byte aligned");
-  const int64_t units = (int64_t)num_tokens * (num_heads + 2 * num_kv_heads);
-  const int64_t blocks = (units + 15) / 16;
-  if (blocks > 0x7fffffff) return fail(SLO_ERR_UNSUPPORTED, "qk_norm_rope_store: too many tokens");
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(qkv), qkv_row_stride, positions, units, num_heads, num_kv_heads,
+  if (num_heads + 2 * num_kv_heads > 16 * QK_UNITS) return fail(SLO_ERR_UNSUPPORTED, "qk_norm_rope_store: more than 64 heads per row");
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)num_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(qkv), qkv_row_stride, positions, num_heads, num_kv_heads,
                      static_cast<const uint16_t*>(q_norm_weight), static_cast<const uint16_t*>(k_norm_weight), eps,
                      cos_sin, max_position, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), slot_mapping,
                      kv_dtype, k_cache, v_cache, k_scale, v_scale, num_slots, scale_floor);

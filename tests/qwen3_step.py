@@ -40,7 +40,7 @@ from torch import nn
 from oracle import attention as oatt
 from oracle import fp8 as ofp8
 from oracle import metadata
-from slo_attn import MixedAttentionContext, get_context, reset_context, set_context
+from slo_attn import MixedAttentionContext, get_context, qk_norm_rope_store, reset_context, set_context
 
 
 @dataclass(frozen=True)
@@ -78,12 +78,12 @@ def add_rms_norm(x, residual, weight, eps):
 
 
 def rope_table(geom: Geometry, device):
-    """rotary_embedding.py:27-35: [max_position, head_dim] fp32 (cos | sin)."""
+    """rotary_embedding.py:27-35: [max_position, head_dim] fp32 (cos | sin), contiguous."""
     d = geom.head_dim
     inv_freq = 1.0 / (geom.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float, device=device) / d))
     t = torch.arange(geom.max_position, dtype=torch.float, device=device)
     freqs = t[:, None] * inv_freq[None, :]
-    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).contiguous()
 
 
 def apply_rope(x, cos, sin):
@@ -128,6 +128,9 @@ class Qwen3:
         self.rope = rope_table(geom, device)
         self.scale = d ** -0.5
         self.attn: list[nn.Module] = []
+        # True: q/k norm, RoPE and the KV write run as one slo_attn launch
+        # (qk_norm_rope_store) and the attention module skips its store.
+        self.fused = False
 
     def forward(self, ids, positions):
         geom = self.geom
@@ -141,12 +144,18 @@ class Qwen3:
             else:
                 h, residual = add_rms_norm(x, residual, w["input_norm"], eps)
             qkv = F.linear(h, w["qkv"])
-            q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
-            q = rms_norm(q.view(-1, hq, d), w["q_norm"], eps)
-            k = rms_norm(k.view(-1, hkv, d), w["k_norm"], eps)
-            v = v.view(-1, hkv, d)
-            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-            o = attn(q, k, v)
+            if self.fused:
+                q, k, v = qk_norm_rope_store(qkv, positions, w["q_norm"], w["k_norm"], eps, self.rope, hq, hkv,
+                                             attn.k_cache, attn.v_cache, get_context().slot_mapping,
+                                             attn.k_scale, attn.v_scale)
+                o = attn(q, k, v, kv_stored=True)
+            else:
+                q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+                q = rms_norm(q.view(-1, hq, d), w["q_norm"], eps)
+                k = rms_norm(k.view(-1, hkv, d), w["k_norm"], eps)
+                v = v.view(-1, hkv, d)
+                q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+                o = attn(q, k, v)
             x = F.linear(o.flatten(1, -1), w["o"])
             h, residual = add_rms_norm(x, residual, w["post_norm"], eps)
             x = F.linear(silu_and_mul(F.linear(h, w["gate_up"])), w["down"])
@@ -331,10 +340,10 @@ class Recorder:
     def __setattr__(self, name, value):
         setattr(self.inner, name, value)
 
-    def __call__(self, q, k, v):
+    def __call__(self, q, k, v, **kw):
         self.seen.append((k.clone(memory_format=torch.contiguous_format),
                           v.clone(memory_format=torch.contiguous_format)))
-        return self.inner(q, k, v)
+        return self.inner(q, k, v, **kw)
 
 
 @torch.inference_mode()

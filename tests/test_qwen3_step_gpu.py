@@ -25,6 +25,10 @@ per-(token, kv head) fp32 scales:
   oracle's store of the K/V that layer was given (E4M3FN codes and fp32 scales
   by ``oracle.fp8.quantize_kv``, evaluated over token slices in threads), and
   every other byte of the pool is unchanged.
+
+The third case runs the HIP side with q/k RMSNorm, RoPE and the KV write fused
+into one launch per layer (slo_attn.qk_norm_rope_store, Attention.forward with
+kv_stored=True); the reference side keeps the reference's separate layers.
 """
 from __future__ import annotations
 
@@ -51,8 +55,9 @@ def _rows(t: torch.Tensor, width: int, slots: torch.Tensor) -> torch.Tensor:
     return t.reshape(-1, width)[slots]
 
 
-@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3fn"])
-def test_qwen3_4b_mixed_step_greedy_and_kv_bytes(device, model, fp8):
+@pytest.mark.parametrize("fp8,fused", [(False, False), (True, False), (True, True)],
+                         ids=["bf16", "e4m3fn", "e4m3fn-fused-qk-norm-rope-store"])
+def test_qwen3_4b_mixed_step_greedy_and_kv_bytes(device, model, fp8, fused):
     geom = model.geom
     hq, hkv, d, layers = geom.num_heads, geom.num_kv_heads, geom.head_dim, geom.num_layers
     batch = config4_batch(geom.vocab)
@@ -62,7 +67,11 @@ def test_qwen3_4b_mixed_step_greedy_and_kv_bytes(device, model, fp8):
     ref_pool, ctl_pool = pool.clone(), pool.clone()
 
     ours = [Recorder(Attention(hq, d, model.scale, hkv)) for _ in range(layers)]
-    logits, tokens = run_step(model, batch, ours, pool)
+    model.fused = fused
+    try:
+        logits, tokens = run_step(model, batch, ours, pool)
+    finally:
+        model.fused = False
     torch.cuda.synchronize()
     print("HIP-path step done", flush=True)
     ref = [ReferenceAttention(hq, d, model.scale, hkv) for _ in range(layers)]
