@@ -40,7 +40,7 @@ from torch import nn
 from oracle import attention as oatt
 from oracle import fp8 as ofp8
 from oracle import metadata
-from slo_attn import MixedAttentionContext, get_context, qk_norm_rope_store, reset_context, set_context
+from slo_attn import KVPool, MixedAttentionContext, get_context, qk_norm_rope_store, reset_context, set_context
 
 
 @dataclass(frozen=True)
@@ -244,43 +244,41 @@ def config4_batch(vocab: int, seed: int = 4, num_blocks: int = 681, block_size: 
 
 # -------------------------------------------------------------------- pools
 class Pool:
-    """KV pool of every layer: bf16, or E4M3FN codes (uint8) plus fp32 scales."""
+    """KV pool of every layer (slo_attn.KVPool: bf16, or E4M3FN codes plus fp32
+    scales) with cached prefixes filled N(0, 1): bf16 values, or their E4M3FN
+    encoding with per-(token, kv head) absmax scales."""
 
     def __init__(self, geom: Geometry, num_blocks: int, block_size: int, device, fp8: bool,
                  seed: int = 1004):
-        shape = (2, geom.num_layers, num_blocks, block_size, geom.num_kv_heads, geom.head_dim)
-        self.fp8 = fp8
+        self.pool = KVPool(geom.num_layers, num_blocks, block_size, geom.num_kv_heads, geom.head_dim,
+                           "fp8_e4m3fn" if fp8 else "bf16", device)
+        self.fp8, self.kv, self.scale = fp8, self.pool.kv, self.pool.scale
+        shape = self.kv.shape
         g = torch.Generator(device=device).manual_seed(seed)
-        if not fp8:
-            self.kv = torch.empty(shape, dtype=torch.bfloat16, device=device)
-            for i in range(2):
-                for l in range(geom.num_layers):
-                    self.kv[i, l].normal_(generator=g)
-            self.scale = None
-            return
-        self.kv = torch.empty(shape, dtype=torch.uint8, device=device)
-        self.scale = torch.empty(shape[:-1], dtype=torch.float32, device=device)
         for i in range(2):
             for l in range(geom.num_layers):
+                if not fp8:
+                    self.kv[i, l].normal_(generator=g)
+                    continue
                 x = torch.empty(shape[2:], dtype=torch.float32, device=device).normal_(generator=g)
                 amax = x.abs().amax(dim=-1)
-                s = torch.where(amax == 0, torch.ones_like(amax), amax / ofp8.FP8_MAX)
-                self.kv[i, l] = (x / s[..., None]).clamp(-ofp8.FP8_MAX, ofp8.FP8_MAX) \
+                sc = torch.where(amax == 0, torch.ones_like(amax), amax / ofp8.FP8_MAX)
+                self.kv[i, l] = (x / sc[..., None]).clamp(-ofp8.FP8_MAX, ofp8.FP8_MAX) \
                     .to(torch.float8_e4m3fn).view(torch.uint8)
-                self.scale[i, l] = s
+                self.scale[i, l] = sc
 
     def clone(self):
         other = object.__new__(Pool)
-        other.fp8, other.kv = self.fp8, self.kv.clone()
-        other.scale = None if self.scale is None else self.scale.clone()
+        other.pool = object.__new__(KVPool)
+        other.pool.__dict__.update(self.pool.__dict__)
+        other.pool.kv = self.kv.clone()
+        other.pool.scale = None if self.scale is None else self.scale.clone()
+        other.fp8, other.kv, other.scale = self.fp8, other.pool.kv, other.pool.scale
         return other
 
     def attach(self, modules):
         """Per-layer views, as allocate_kv_cache assigns them (mixed_model_runner.py:43-47)."""
-        for l, m in enumerate(modules):
-            m.k_cache, m.v_cache = self.kv[0, l], self.kv[1, l]
-            if self.fp8:
-                m.k_scale, m.v_scale = self.scale[0, l], self.scale[1, l]
+        assert self.pool.attach(modules) == self.pool.num_layers
 
 
 class ReferenceAttention(nn.Module):
