@@ -95,6 +95,25 @@ int slo_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_
                            int64_t num_slots, float scale_floor, slo_stream_t stream);
 
 /*
+ * LM head on the sampled rows with the greedy argmax fused in.
+ *
+ * Replaces compute_logits on the sampled hidden rows and the greedy argmax of
+ * run_mixed (nanovllm/engine/mixed_model_runner.py:115-126; ParallelLMHead,
+ * nanovllm/layers/embed_head.py:56-66, at TP=1): for each of num_rows rows of
+ * `hidden` (bf16, rows `hidden_row_stride` apart), logits[r, v] =
+ * bf16(sum_k hidden[r, k] * weight[v, k]) with fp32 sums over the bf16
+ * `weight` [vocab_size, hidden_size] (rows `weight_row_stride` apart), and
+ * tokens[r] (int64) = the first v with the largest logits[r, v].  `logits`
+ * [num_rows, >= vocab_size] bf16 is written only when not NULL.  `keys` is a
+ * uint64 [num_rows] scratch array that must be zero before the first call;
+ * every call leaves it zero.  num_rows <= 128; hidden_size a multiple of 128.
+ */
+int slo_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, int32_t num_rows,
+                       const void* weight, int64_t weight_row_stride, int32_t vocab_size,
+                       int32_t hidden_size, void* logits, int64_t logits_row_stride,
+                       uint64_t* keys, int64_t* tokens, slo_stream_t stream);
+
+/*
  * Arguments of one ragged paged-attention launch.  Query rows [0, num_decode)
  * are decode rows (one query each, attending to decode_lens[b] cached tokens
  * through decode_tables[b]); query rows num_decode + [cu_q[r], cu_q[r+1]) are

@@ -176,6 +176,46 @@ def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight
     return q, k, v
 
 
+# ------------------------------------------------------ LM head + greedy argmax
+_keys: dict[int, torch.Tensor] = {}
+LM_HEAD_MAX_ROWS = 128
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, return_logits: bool = False):
+    """Greedy next tokens of the sampled rows: argmax_v bf16(hidden[r] . weight[v]).
+
+    compute_logits + argmax of run_mixed (nanovllm/engine/mixed_model_runner.py:
+    115-126, nanovllm/layers/embed_head.py:56-66) in one pass over the weight.
+    ``hidden``: ``[rows, hidden_size]`` bf16 (the already-selected sampled rows,
+    at most 128); ``weight``: ``[vocab, hidden_size]`` bf16.  Returns int64
+    ``[rows]`` tokens (ties: the smallest index), and the bf16 logits
+    ``[rows, vocab]`` as well when ``return_logits``.
+    """
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("hidden must be [rows, hidden_size] and weight [vocab, hidden_size]")
+    device = _require_gpu(hidden, weight)
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("hidden and weight must be bf16")
+    if hidden.stride(-1) != 1 or weight.stride(-1) != 1:
+        raise ValueError("hidden and weight rows must be contiguous")
+    rows, vocab = hidden.shape[0], weight.shape[0]
+    if rows > LM_HEAD_MAX_ROWS:
+        raise ValueError(f"at most {LM_HEAD_MAX_ROWS} sampled rows per call")
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    keys = _keys.get(index)
+    if keys is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("call lm_head_argmax once before graph capture")
+        keys = torch.zeros(LM_HEAD_MAX_ROWS, dtype=torch.int64, device=device)
+        _keys[index] = keys
+    tokens = torch.empty(rows, dtype=torch.int64, device=device)
+    logits = torch.empty(rows, vocab, dtype=torch.bfloat16, device=device) if return_logits else None
+    _lib.check(_lib.load().slo_lm_head_argmax(
+        _ptr(hidden), hidden.stride(0), rows, _ptr(weight), weight.stride(0), vocab, hidden.shape[1], _ptr(logits),
+        vocab, _ptr(keys), _ptr(tokens), _stream(device)), "slo_lm_head_argmax")
+    return (tokens, logits) if return_logits else tokens
+
+
 # ---------------------------------------------------------------- workspace
 _ws_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}

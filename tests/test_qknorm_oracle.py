@@ -1,4 +1,5 @@
-"""Pins the CPU definition of q/k RMSNorm + RoPE + KV write (oracle/qknorm.py).
+"""Pins the CPU definitions of q/k RMSNorm + RoPE + KV write (oracle/qknorm.py)
+and of the LM head with greedy argmax (oracle/lm_head.py).
 
 * rope: bit-exact against the reference's own formula evaluated by torch on
   the CPU (nanovllm/layers/rotary_embedding.py:6-14, eager: every product and
@@ -17,6 +18,9 @@
   halfway values.
 * qkv_step: splits the fused QKV row as qkv.split([q, k, v]) does
   (qwen3.py:79-81) and leaves v untouched.
+* lm_head.logits: within one bf16 step of torch's F.linear on the CPU (the
+  reference's compute_logits) on all elements, equal on all but ~1%;
+  lm_head.greedy: torch.argmax's first-index rule on exact ties.
 """
 import numpy as np
 import torch
@@ -121,3 +125,26 @@ def test_qkv_step_splits_rows_and_keeps_v():
     cos, sin = table[pos, :HD // 2].numpy(), table[pos, HD // 2:].numpy()
     assert np.array_equal(q, qknorm.rope(qknorm.rms_norm(_bits(qv.reshape(n, hq, HD)), _bits(w), EPS), cos, sin))
     assert np.array_equal(k, qknorm.rope(qknorm.rms_norm(_bits(kv_.reshape(n, hkv, HD)), _bits(w), EPS), cos, sin))
+
+
+# ------------------------------------------------- LM head + greedy (oracle/lm_head.py)
+def test_lm_head_oracle_against_torch_and_tie_rule():
+    from oracle import lm_head
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(9, 512, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(3000, 512, generator=g)).to(torch.bfloat16)
+    got = lm_head.logits(_bits(h), _bits(w))
+    # the reference computation (F.linear in bf16), evaluated by torch on the CPU
+    want = torch.nn.functional.linear(h, w)
+    diff = (_from_bits(got).float() - want.float()).abs()
+    ulp = torch.ldexp(torch.ones_like(diff), torch.frexp(want.float().abs().clamp_min(1e-30))[1] - 8)
+    assert (diff <= ulp).all() and (diff > 0).float().mean() < 1e-2
+    # ties: identical weight rows give identical logits; the first index wins, as in torch.argmax
+    w2 = w.clone()
+    w2[2000] = w2[100]
+    lg = lm_head.logits(_bits(h), _bits(w2))
+    top = lm_head.greedy(lg)
+    assert np.array_equal(top, torch.argmax(_from_bits(lg).float(), dim=-1).numpy())
+    h3 = w2[100:101].clone() * 4  # row aligned with the duplicated weight row
+    t3 = lm_head.greedy(lm_head.logits(_bits(h3.to(torch.bfloat16)), _bits(w2)))
+    assert t3[0] == 100
