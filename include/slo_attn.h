@@ -114,6 +114,30 @@ int slo_lm_head_argmax(const void* hidden, int64_t hidden_row_stride, int32_t nu
                        uint64_t* keys, int64_t* tokens, slo_stream_t stream);
 
 /*
+ * Mixed-step metadata on the GPU, capacity-padded for graph replay.
+ *
+ * Replaces the host loops of build_batch (nanovllm/engine/batch_metadata.py:
+ * 94-118) and prepare_mixed (nanovllm/engine/mixed_model_runner.py:58-92).
+ * Rows [0, decode_capacity) are decode rows (row_tokens 1, or 0 for an unused
+ * row), rows [decode_capacity, decode_capacity + prefill_capacity) prefill
+ * rows (row_tokens >= 0); row_start is each row's first new position and
+ * tables its block table ([rows, >= table_width], -1 padded).  Token b is
+ * decode row b; token decode_capacity + cu_seqlens_q[r] + i is token i of
+ * prefill row r.  Writes positions (int64) and slot_mapping for
+ * token_capacity tokens (slot -1, position 0 past the rows' tokens),
+ * decode_lens (end_pos, 0 for unused rows), cu_seqlens_q / cu_seqlens_k
+ * [prefill_capacity + 1] (sums of num_tokens / end_pos) and last_token
+ * [decode_capacity + prefill_capacity] (-1 for rows without tokens).  At most
+ * 1024 prefill rows.
+ */
+int slo_build_mixed_metadata(const int32_t* row_start, const int32_t* row_tokens,
+                             int32_t decode_capacity, int32_t prefill_capacity,
+                             int32_t token_capacity, const int32_t* tables, int32_t table_stride,
+                             int32_t table_width, int32_t block_size, int64_t* positions,
+                             int32_t* slot_mapping, int32_t* decode_lens, int32_t* cu_seqlens_q,
+                             int32_t* cu_seqlens_k, int32_t* last_token, slo_stream_t stream);
+
+/*
  * Arguments of one ragged paged-attention launch.  Query rows [0, num_decode)
  * are decode rows (one query each, attending to decode_lens[b] cached tokens
  * through decode_tables[b]); query rows num_decode + [cu_q[r], cu_q[r+1]) are

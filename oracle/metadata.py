@@ -46,3 +46,49 @@ def mixed_metadata(decode_end_pos, decode_tables, prefill_start, prefill_count, 
         "max_k": max(s + n for s, n in zip(prefill_start, prefill_count)) if prefill_count else 0,
         "prefill_has_history": any(s > 0 for s in prefill_start),
     }
+
+
+def padded_step(row_start, row_tokens, decode_capacity, prefill_capacity, token_capacity, tables, block_size):
+    """Capacity-padded metadata of one mixed step (host lists).
+
+    Rows [0, Dc) are decode rows (1 token, 0 for an unused row), rows
+    [Dc, Dc + Pc) prefill rows; token b is decode row b, token Dc + cu_q[r] + i
+    is token i of prefill row r, at position start + i, with the slot formula
+    of build_batch (batch_metadata.py:105); decode_lens holds end_pos
+    (mixed_model_runner.py:83); cu_q / cu_k accumulate num_tokens / end_pos
+    over prefill rows (:75-78), with 0 for a row without tokens; every other
+    token has slot -1 and position 0.
+    """
+    dc, pc = decode_capacity, prefill_capacity
+
+    def slot(row, pos):
+        t = tables[row]
+        idx = pos // block_size
+        if pos < 0 or idx >= len(t) or t[idx] < 0:
+            return -1
+        return t[idx] * block_size + pos % block_size
+
+    positions = [0] * token_capacity
+    slots = [-1] * token_capacity
+    decode_lens = [0] * dc
+    last = [-1] * (dc + pc)
+    for b in range(dc):
+        if row_tokens[b] > 0:
+            positions[b] = row_start[b]
+            slots[b] = slot(b, row_start[b])
+            decode_lens[b] = row_start[b] + 1
+            last[b] = b
+    cu_q, cu_k = [0], [0]
+    for r in range(pc):
+        n = max(row_tokens[dc + r], 0)
+        for i in range(n):
+            t = dc + cu_q[-1] + i
+            if t < token_capacity:
+                positions[t] = row_start[dc + r] + i
+                slots[t] = slot(dc + r, row_start[dc + r] + i)
+        if n:
+            last[dc + r] = dc + cu_q[-1] + n - 1
+        cu_q.append(cu_q[-1] + n)
+        cu_k.append(cu_k[-1] + (row_start[dc + r] + n if n else 0))
+    return {"positions": positions, "slot_mapping": slots, "decode_lens": decode_lens,
+            "cu_seqlens_q": cu_q, "cu_seqlens_k": cu_k, "last_token": last}

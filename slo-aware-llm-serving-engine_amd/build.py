@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "slo_attn")
 LIB = os.path.join(OUT_DIR, "libslo_attn.so")
-SOURCES = ["store_kv.hip", "qk_norm_rope.hip", "lm_head.hip", "paged_attention.hip", "capi.cpp"]
+SOURCES = ["store_kv.hip", "qk_norm_rope.hip", "lm_head.hip", "metadata.hip", "paged_attention.hip", "capi.cpp"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",

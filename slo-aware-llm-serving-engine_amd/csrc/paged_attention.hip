@@ -129,6 +129,10 @@ struct Params {
   int* ctrl;      // per list: [0] fetch counter (zero between launches)
   int* counters;  // split-K tickets, [num_decode * hkv]
   float* partials;
+  // Query rows past every decode and prefill row of the arguments (whatever
+  // the phases) start at q_off_prefill + cu_q_all[np_all]; they get zeros.
+  const int32_t* cu_q_all;
+  int32_t np_all;
 };
 
 // The two tile stages live in two separate __shared__ arrays of STAGE_BYTES
@@ -1481,6 +1485,18 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     __syncthreads();
   }
   if constexpr (HAS_DEC) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
+
+  // Rows that belong to no decode or prefill row (the capacity padding of a
+  // captured step) get zeros, so every output row is defined.
+  const int64_t covered = (int64_t)p.q_off_prefill + (p.np_all > 0 ? max(p.cu_q_all[p.np_all], 0) : 0);
+  if (covered < p.num_q_rows) {
+    const int per_row = p.hkv * p.G * HD / 8;  // 16-byte pieces per output row
+    const int64_t pieces = (p.num_q_rows - covered) * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * NT + tid; i < pieces; i += (int64_t)gridDim.x * NT) {
+      const int64_t row = covered + i / per_row;
+      *reinterpret_cast<u32x4*>(p.out + row * p.out_stride + 8 * (i % per_row)) = u32x4{0, 0, 0, 0};
+    }
+  }
 }
 
 struct DeviceShape {
@@ -1626,6 +1642,8 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   p.ctrl = reinterpret_cast<int*>(ws);
   p.counters = reinterpret_cast<int*>(ws + CTRL_BYTES);
   p.partials = reinterpret_cast<float*>(ws + PARTIALS_OFFSET);
+  p.cu_q_all = a->num_prefill > 0 ? a->prefill_cu_q : nullptr;
+  p.np_all = a->num_prefill > 0 && a->prefill_cu_q ? a->num_prefill : 0;
 
   // Upper bound on the item count from host-known shapes only.
   int64_t bound = 0;

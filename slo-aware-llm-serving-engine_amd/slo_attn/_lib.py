@@ -62,6 +62,7 @@ EXPORTS = (
     "slo_store_kvcache",
     "slo_qk_norm_rope_store",
     "slo_lm_head_argmax",
+    "slo_build_mixed_metadata",
     "slo_attention_workspace_bytes",
     "slo_paged_attention",
     "slo_last_error",
@@ -95,6 +96,10 @@ def load() -> ctypes.CDLL:
         lib.slo_lm_head_argmax.argtypes = [
             _c_void_p, _c_int64, _c_int32, _c_void_p, _c_int64, _c_int32, _c_int32, _c_void_p, _c_int64,
             _c_void_p, _c_void_p, _c_void_p]
+        lib.slo_build_mixed_metadata.restype = ctypes.c_int
+        lib.slo_build_mixed_metadata.argtypes = [
+            _c_void_p, _c_void_p, _c_int32, _c_int32, _c_int32, _c_void_p, _c_int32, _c_int32, _c_int32,
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
         lib.slo_attention_workspace_bytes.restype = ctypes.c_int
         lib.slo_attention_workspace_bytes.argtypes = [
             _c_int32, _c_int32, _c_int32, _c_int32, _c_int32, ctypes.POINTER(ctypes.c_size_t)]

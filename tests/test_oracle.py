@@ -280,3 +280,26 @@ def test_store_fp8_matches_quantize_per_head():
         c, sc = fp8.quantize_kv(k[i])
         assert np.array_equal(kc[s // bs, s % bs], c) and np.array_equal(ks[s // bs, s % bs], sc)
     assert (kc[0, 1] == 0).all()  # slot of the -1 row never written
+
+
+def test_padded_step_metadata_matches_prepare_mixed_and_slot_kats():
+    # unpadded rows agree with mixed_metadata (prepare_mixed) and with expected_slots
+    # (layer_replay.py:32-37); padding rows and tokens are inert.
+    tables = [[2, 0], [5], [1, 3, 4], [6]]
+    dstart = [300, 17]
+    rows = [(250, 20), (0, 5)]
+    dc, pc, tc, bs = 3, 3, 40, 256
+    starts = dstart + [0] + [s for s, _ in rows] + [0]
+    toks = [1, 1, 0] + [n for _, n in rows] + [0]
+    tabs = tables[:2] + [[]] + tables[2:] + [[]]
+    got = metadata.padded_step(starts, toks, dc, pc, tc, tabs, bs)
+    ref = metadata.mixed_metadata([301, 18], tables[:2], [250, 0], [20, 5], tables[2:])
+    assert got["decode_lens"] == ref["decode_lens"] + [0]
+    assert got["cu_seqlens_q"] == ref["prefill_cu_q"] + [25]
+    assert got["cu_seqlens_k"] == ref["prefill_cu_k"] + [ref["prefill_cu_k"][-1]]
+    assert got["slot_mapping"][:2] == [metadata.slot_of(tables[0], 300, bs), metadata.slot_of(tables[1], 17, bs)]
+    assert got["slot_mapping"][2] == -1
+    assert got["slot_mapping"][3:23] == metadata.expected_slots(tables[2], 250, 270, bs)
+    assert got["slot_mapping"][23:28] == metadata.expected_slots(tables[3], 0, 5, bs)
+    assert got["slot_mapping"][28:] == [-1] * 12 and got["positions"][28:] == [0] * 12
+    assert got["positions"][3:5] == [250, 251] and got["last_token"] == [0, 1, -1, 22, 27, -1]
