@@ -20,6 +20,9 @@ slot-mapped KV write of the 1048 new tokens + ONE ragged attention launch.
   flash-attn calls.
 * roofline_qk_norm_rope_store: the step before attention (q/k RMSNorm, RoPE
   and the KV write fused into one launch) on the same new tokens, against HBM.
+* roofline_lm_head_argmax: the step after the model (LM head + greedy argmax
+  fused, Qwen3-4B head 151936 x 2560 bf16) on the step's 26 sampled rows,
+  against HBM (the weight read dominates).
 * cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
   step.
 """
@@ -38,6 +41,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+# spin kernel queued ahead of each event-timed launch (about 0.4 ms): longer than
+# the host time of any launch call here, so the GPU never waits for the host
+# inside an event pair
+SPIN_CYCLES = 1_000_000
 METRIC = "mixed-step attn tokens/s; decode KV HBM GB/s (% of peak); prefill MFMA util"
 
 
@@ -49,8 +56,8 @@ def parse():
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16")
     ap.add_argument("--events", type=int, default=100, help="event-timed launches per mode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile", choices=["fused", "decode", "prefill"], default=None,
-                    help="only launch this attention phase (for rocprofv3 counter runs), plus one "
+    ap.add_argument("--profile", choices=["fused", "decode", "prefill", "qk", "lm_head"], default=None,
+                    help="only launch this attention phase or kernel (for rocprofv3 counter runs), plus one "
                          "256 MiB device copy whose counters calibrate FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
@@ -62,7 +69,8 @@ def main():
               "(the attention path runs at TP=1 and this build has no multi-GPU path).", file=sys.stderr)
         sys.exit(2)
     import torch
-    from slo_attn import _lib, forward_mixed, qk_norm_rope_store, reserve_workspace, rope_cos_sin, store_kvcache, workloads
+    from slo_attn import (_lib, forward_mixed, lm_head_argmax, qk_norm_rope_store, reserve_workspace, rope_cos_sin,
+                          store_kvcache, workloads)
     from slo_attn.ops import paged_attention
     from types import SimpleNamespace
 
@@ -106,26 +114,76 @@ def main():
             prefill_cu_k=meta.prefill_cu_k, max_q=meta.max_q, max_k=meta.max_k,
             prefill_tables=meta.prefill_tables, phases=phases, out=out_buf)
 
-    out_buf = torch.empty_like(q)
-    if args.profile:
-        phase = {"fused": _lib.PHASE_ALL, "decode": _lib.PHASE_DECODE, "prefill": _lib.PHASE_PREFILL}[args.profile]
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=device)
-        dst = torch.empty_like(src)
-        dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+    hq, hkv, d = 32, 8, 128
+    elem = 1.0 if fp8 else 2.0
+    scale_b = 4 if fp8 else 0
+    tokens = w.num_tokens
+
+    # ---- the step before attention: fused q/k RMSNorm + RoPE + KV write of the
+    # same new tokens from a synthetic QKV projection output [tokens, 48*128]
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(tokens, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(device)
+    positions = [L - 1 for L in w.decode_lens]
+    for n, pfx in zip(w.prefill_q, w.prefill_prefix):
+        positions += list(range(pfx, pfx + n))
+    positions = torch.tensor(positions, dtype=torch.int64, device=device)
+    qn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    kn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    cos_sin = rope_cos_sin(d, 40960, 1e6, device)
+
+    def qk_launch(i):
+        kc, vc, ks, vs = pools[i % nsets]
+        qk_norm_rope_store(qkv, positions, qn_w, kn_w, 1e-6, cos_sin, hq, hkv, kc, vc, slots, ks, vs)
+
+    # read the QKV row, positions and one cos/sin row per token; write q, k and the K/V pool entries
+    qk_bytes = tokens * ((hq + 2 * hkv) * d * 2 + 8 + d * 4 + 4 + (hq + hkv) * d * 2 + 2 * hkv * (d * elem + scale_b))
+
+    # ---- the step after the model: LM head + greedy argmax on the step's sampled
+    # rows (every decode row and the last token of each prefill chunk) over the
+    # Qwen3-4B head [151936, 2560]; two weight copies alternate so each launch
+    # streams its 778 MB weight from HBM
+    vocab, hidden = 151936, 2560
+    sample_rows = w.num_decode + len(w.prefill_q)
+    heads = []
+    if args.profile in (None, "lm_head"):
+        gd = torch.Generator(device=device).manual_seed(6)
+        heads = [torch.empty(vocab, hidden, dtype=torch.bfloat16, device=device).normal_(0, 0.02, generator=gd)
+                 for _ in range(2)]
+        hid = torch.empty(sample_rows, hidden, dtype=torch.bfloat16, device=device).normal_(0, 1, generator=gd)
+
+    def lm_launch(i):
+        lm_head_argmax(hid, heads[i % 2])
+
+    # weight + sampled hidden rows read, one int64 token per row written
+    lm_bytes = vocab * hidden * 2 + sample_rows * hidden * 2 + sample_rows * 8
+
+    def timed(fn, warmup=3, n=None):
+        """Average HIP-event duration of fn(i) on the current stream; a spin kernel
+        queued ahead keeps host launch latency out of the interval."""
         times = []
-        for i in range(args.warmup + args.events):
-            torch.cuda._sleep(200_000)
+        for i in range(warmup + (args.events if n is None else n)):
+            torch.cuda._sleep(SPIN_CYCLES)
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-            attn_only(i, phase)
+            fn(i)
             e1.record()
             e1.synchronize()
-            if i >= args.warmup:
+            if i >= warmup:
                 times.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.mean(times)
+
+    out_buf = torch.empty_like(q)
+    if args.profile:
+        launch = {"fused": lambda i: attn_only(i, _lib.PHASE_ALL), "decode": lambda i: attn_only(i, _lib.PHASE_DECODE),
+                  "prefill": lambda i: attn_only(i, _lib.PHASE_PREFILL), "qk": qk_launch,
+                  "lm_head": lm_launch}[args.profile]
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+        avg = timed(launch, args.warmup, args.events)
         print(json.dumps({"profile": args.profile, "launches": args.warmup + args.events,
-                          "avg_launch_us": round(statistics.mean(times), 2),
-                          "median_launch_us": round(statistics.median(times), 2)}))
+                          "avg_launch_us": round(avg, 2)}))
         return
     for i in range(max(args.warmup, 4)):
         step(i)
@@ -154,7 +212,6 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / steps
-    tokens = w.num_tokens
     value = tokens * steps / elapsed
 
     # ---- per-launch kernel durations (HIP events on the launch stream, cold cache)
@@ -162,7 +219,7 @@ def main():
         stream = torch.cuda.current_stream()
         times = []
         for i in range(args.events + 3):
-            torch.cuda._sleep(200_000)  # GPU-side backlog: the events bracket only the launch
+            torch.cuda._sleep(SPIN_CYCLES)  # GPU-side backlog: the events bracket only the launch
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(stream)
@@ -177,10 +234,7 @@ def main():
     t_dec, t_dec_med = launch_times(_lib.PHASE_DECODE)
     t_pre, t_pre_med = launch_times(_lib.PHASE_PREFILL)
 
-    elem = 1.0 if fp8 else 2.0
-    scale_b = 4 if fp8 else 0
     dec_bytes = w.decode_kv_bytes(elem, scale_b)
-    hq, hkv, d = 32, 8, 128
     pre_kv_tokens = sum(n + p for n, p in zip(w.prefill_q, w.prefill_prefix))
     pre_bytes = pre_kv_tokens * hkv * (2 * d * elem + 2 * scale_b)
     qo_bytes = 2 * tokens * hq * d * 2
@@ -190,41 +244,22 @@ def main():
     dec_gbs = (dec_bytes + 2 * w.num_decode * hq * d * 2) / (t_dec * 1e-6) / 1e9
     pre_tflops = flops / (t_pre * 1e-6) / 1e12
 
-    # ---- the step before attention: fused q/k RMSNorm + RoPE + KV write of the
-    # same new tokens from a synthetic QKV projection output [tokens, 48*128]
-    g = torch.Generator().manual_seed(5)
-    qkv = torch.randn(tokens, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(device)
-    positions = [L - 1 for L in w.decode_lens]
-    for n, pfx in zip(w.prefill_q, w.prefill_prefix):
-        positions += list(range(pfx, pfx + n))
-    positions = torch.tensor(positions, dtype=torch.int64, device=device)
-    qn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
-    kn_w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
-    cos_sin = rope_cos_sin(d, 40960, 1e6, device)
-    qk_times = []
-    for i in range(args.events + 3):
-        kc, vc, ks, vs = pools[i % nsets]
-        torch.cuda._sleep(200_000)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        qk_norm_rope_store(qkv, positions, qn_w, kn_w, 1e-6, cos_sin, hq, hkv, kc, vc, slots, ks, vs)
-        e1.record()
-        e1.synchronize()
-        if i >= 3:
-            qk_times.append(e0.elapsed_time(e1) * 1e3)
-    t_qk = statistics.mean(qk_times)
-    # read the QKV row, positions and one cos/sin row per token; write q, k and the K/V pool entries
-    qk_bytes = tokens * ((hq + 2 * hkv) * d * 2 + 8 + d * 4 + 4 + (hq + hkv) * d * 2 + 2 * hkv * (d * elem + scale_b))
+    t_qk = timed(qk_launch)
     qk_gbs = qk_bytes / (t_qk * 1e-6) / 1e9
+    t_lm = timed(lm_launch)
+    lm_gbs = lm_bytes / (t_lm * 1e-6) / 1e9
+    del heads
 
     # HBM bytes per fused launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE,
     # calibrated against a 256 MiB copy) for this kernel, kept under profiles/.
-    traffic = None
+    measured = {}
     tpath = os.path.join(ROOT, "profiles", "traffic_mixed_24decode_2x512chunk.json")
     if not fp8 and os.path.exists(tpath):
         with open(tpath) as fh:
-            traffic = round(json.load(fh)["fused"]["traffic_mb"] * 1e6)
+            measured = json.load(fh)
+
+    def traffic(kernel):
+        return round(measured[kernel]["traffic_mb"] * 1e6) if kernel in measured else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -251,7 +286,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(fused_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": traffic("fused"),
             "kernel": "paged_attention_kernel (fused decode+prefill)",
             "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(t_fused, 2),
             "median_launch_us": round(t_fused_med, 2),
@@ -269,9 +304,15 @@ def main():
         "split_step_us": round(t_dec + t_pre, 2),
         "roofline_qk_norm_rope_store": {
             "bound": "hbm", "achieved": round(qk_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(qk_gbs / HBM_PEAK_GBS, 4), "kernel": "qk_norm_rope_store_kernel",
+            "frac": round(qk_gbs / HBM_PEAK_GBS, 4), "traffic": traffic("qk"), "kernel": "qk_norm_rope_store_kernel",
             "algorithmic_bytes_per_launch": qk_bytes, "avg_launch_us": round(t_qk, 2),
             "tokens": tokens,
+        },
+        "roofline_lm_head_argmax": {
+            "bound": "hbm", "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic("lm_head"), "kernel": "lm_head_argmax_kernel",
+            "algorithmic_bytes_per_launch": lm_bytes, "avg_launch_us": round(t_lm, 2),
+            "rows": sample_rows, "vocab": vocab, "hidden": hidden,
         },
         "cpu_baseline": cpu,
     }
