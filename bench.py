@@ -248,6 +248,8 @@ def main():
     qk_gbs = qk_bytes / (t_qk * 1e-6) / 1e9
     t_lm = timed(lm_launch)
     lm_gbs = lm_bytes / (t_lm * 1e-6) / 1e9
+    # the reference's path on the same inputs: compute_logits (F.linear) then argmax
+    t_lm_torch = timed(lambda i: torch.nn.functional.linear(hid, heads[i % 2]).argmax(dim=-1))
     del heads
 
     # HBM bytes per fused launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE,
@@ -313,6 +315,7 @@ def main():
             "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic("lm_head"), "kernel": "lm_head_argmax_kernel",
             "algorithmic_bytes_per_launch": lm_bytes, "avg_launch_us": round(t_lm, 2),
             "rows": sample_rows, "vocab": vocab, "hidden": hidden,
+            "torch_linear_argmax_us": round(t_lm_torch, 2),
         },
         "cpu_baseline": cpu,
     }
