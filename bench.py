@@ -157,9 +157,10 @@ def main():
     # weight + sampled hidden rows read, one int64 token per row written
     lm_bytes = vocab * hidden * 2 + sample_rows * hidden * 2 + sample_rows * 8
 
-    def timed(fn, warmup=3, n=None):
+    def timed(fn, warmup=None, n=None):
         """Average HIP-event duration of fn(i) on the current stream; a spin kernel
         queued ahead keeps host launch latency out of the interval."""
+        warmup = args.warmup if warmup is None else warmup
         times = []
         for i in range(warmup + (args.events if n is None else n)):
             torch.cuda._sleep(SPIN_CYCLES)
@@ -218,7 +219,7 @@ def main():
     def launch_times(phases):
         stream = torch.cuda.current_stream()
         times = []
-        for i in range(args.events + 3):
+        for i in range(args.events + args.warmup):
             torch.cuda._sleep(SPIN_CYCLES)  # GPU-side backlog: the events bracket only the launch
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
@@ -226,7 +227,7 @@ def main():
             attn_only(i, phases)
             e1.record(stream)
             e1.synchronize()
-            if i >= 3:
+            if i >= args.warmup:
                 times.append(e0.elapsed_time(e1) * 1e3)  # us
         return statistics.mean(times), statistics.median(times)
 

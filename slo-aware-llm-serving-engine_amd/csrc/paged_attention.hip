@@ -1044,7 +1044,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // tile is in flight while the current one is consumed; E4M3FN pool bytes are
   // loaded into registers, decoded, and written to LDS after the current tile's
   // compute.  Rows past the valid keys are zero.
-  u32x4 kr[4], vr[4];
+  u32x2 kr[4], vr[4];  // E4M3FN tiles: raw code bytes, converted when committed to LDS
   float ksr = 0.0f, vsr = 0.0f;
   const int* prow = p.ptab + (int64_t)r * p.ptab_stride;
   const int npages = paged ? (kend + p.block_size - 1) / p.block_size : 0;
@@ -1080,10 +1080,10 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int row = (tid >> 4) + 16 * it;
-        u32x4 kx = u32x4{0, 0, 0, 0}, vx = u32x4{0, 0, 0, 0};
+        u32x2 kx = u32x2{0, 0}, vx = u32x2{0, 0};  // code 0 decodes to +0
         if (row < nv) {
-          kx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.k_cache) + kbase + kgo[it]));
-          vx = fp8x8_to_bf16x8(ld8(static_cast<const uint8_t*>(p.v_cache) + vbase + vgo[it]));
+          kx = ld8(static_cast<const uint8_t*>(p.k_cache) + kbase + kgo[it]);
+          vx = ld8(static_cast<const uint8_t*>(p.v_cache) + vbase + vgo[it]);
         }
         kr[it] = kx;
         vr[it] = vx;
@@ -1123,13 +1123,15 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       }
     }
   };
-  auto commit_tile = [&](int buf) {  // register-staged (E4M3FN) tiles only
+  // Register-staged (E4M3FN) tiles only: the code bytes loaded by issue_tile
+  // (in flight during the current tile's compute) are decoded to bf16 here.
+  auto commit_tile = [&](int buf) {
     if (!src_fp8) return;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
-      st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), kr[it]);
-      st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), vr[it]);
+      st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(kr[it]));
+      st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(vr[it]));
     }
     if (tid < TT) {
       sm.u.pf.ks[buf][tid] = ksr;
@@ -1652,11 +1654,15 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
     const int64_t tq = std::max<int64_t>(0, a->num_q_rows - a->num_decode);
     bound += (tq / BQ_MIN + p.np) * p.hkv * p.HG;
   }
-  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8 ? 1 : 0];
+  // The E4M3FN instantiation only where the launch reads the pool: a launch of
+  // cold prefill rows (new K/V only) runs the bf16 one, which holds fewer
+  // registers.
+  const bool fp8_reads = fp8 && (do_dec || (do_pf && p.ptab != nullptr));
+  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8_reads ? 1 : 0];
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
-  switch (mode + 3 * (fp8 ? 1 : 0)) {
+  switch (mode + 3 * (fp8_reads ? 1 : 0)) {
     case 0: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
     case 1: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;
     case 2: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_DECODE>), dim3(grid), dim3(NT), 0, s, p); break;
