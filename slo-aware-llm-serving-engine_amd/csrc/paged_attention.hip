@@ -161,6 +161,7 @@ struct Smem {
   uint32_t item;
   int row;
   int salt;
+  int split_tiles;  // E4M3FN mixed launches: rows with a heavier 32-position block use 16
   int meta[2][8];   // decode: landed row length and block-table entries, by item parity
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
@@ -1302,19 +1303,21 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // Item counts of this thread's rows under either choice (32-position
   // blocks / CHUNK, 16-position blocks / CHUNK_MIN), so the metadata is read
   // once.
-  int cnt_a[4], cnt_b[4];
+  int cnt_a[4], cnt_b[4], tmr[4];
   {
     int w = 0, tm = 0, dn = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = r0 + i;
       cnt_a[i] = cnt_b[i] = 0;
+      tmr[i] = 0;
       if (i >= per || r >= nrows) continue;
       if (r < p.np) {
         int wr, tr;
         pf_work(p, r, wr, tr);
         w += wr;
         tm = max(tm, tr);
+        tmr[i] = tr;
         const int lq = p.cu_q[r + 1] - p.cu_q[r];
         cnt_a[i] = lq > 0 ? ((lq + 31) / 32) * p.hkv * p.HG : 0;
         cnt_b[i] = lq > 0 ? ((lq + 15) / 16) * p.hkv * p.HG : 0;
@@ -1348,6 +1351,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     }
     if (MODE == MODE_PREFILL && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
     if (dt * p.hkv < 2 * (int64_t)gridDim.x) dchunk = CHUNK_MIN;
+    // E4M3FN mixed launches: a prefill row whose heaviest 32-position block
+    // spans more key tiles than a workgroup's share of the launch (a decode
+    // item counted as 4 tiles) uses 16-position blocks, which halves the
+    // longest items; register-staged E4M3FN tiles make those items the
+    // launch's critical path.  (With bf16 pools the extra tile reads cost
+    // more than the shorter items gain.)
+    if (tid == 0)
+      sm.split_tiles = (FP8 && MODE == MODE_MIXED) ? (int)((4 * dt * p.hkv + wt) / gridDim.x) : (1 << 30);
     __syncthreads();
   }
 
@@ -1356,7 +1367,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   int local_sum = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool alt = r0 + i < p.np ? bq == 16 : dchunk == CHUNK_MIN;
+    const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == CHUNK_MIN;
     cnt[i] = alt ? cnt_b[i] : cnt_a[i];
     local_sum += cnt[i];
   }
@@ -1466,7 +1477,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
           if (bq == 16) prefill_item<FP8, 1>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
           else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
         } else if constexpr (HAS_PF) {
-          prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          int wr = 0, tr = 0;
+          if constexpr (FP8) pf_work(p, r, wr, tr);
+          if (FP8 && tr > sm.split_tiles) prefill_item<FP8, FP8 ? 1 : 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
         }
         // The next item is fetched only now: fetching ahead would let a
         // workgroup claim a second item before a late-starting one takes its
