@@ -4,13 +4,17 @@ Workload: the V1 mixed ragged batch of Qwen3-4B attention (32 query heads,
 8 kv heads, head_dim 128, 256-token pages): 24 decode rows with contexts drawn
 uniform in [256, 4096] (seed 3) plus two 512-token prefill chunks with cached
 prefixes 0 and 1024, 1048 new tokens, 512-page pool.  One step = the
-slot-mapped KV write of the 1048 new tokens + ONE ragged attention launch.
+slot-mapped KV write of the 1048 new tokens + the ragged attention, as
+forward_mixed runs them: with a bf16 pool ONE launch that also writes the new
+K/V (the new tokens are read from their rows), with an E4M3FN pool the store
+kernel and then one attention launch.
 
 * value: whole-step throughput in tokens/s (1048 tokens per step), from HIP
   graph replays of 4 consecutive steps that rotate over 4 copies of the pool
   (4 x 512 MiB) so that no step finds its KV in the 256 MB Infinity Cache.
 * roofline: the fused attention kernel against HBM bandwidth; achieved =
-  algorithmic bytes per launch (decode KV bytes + prefill K/V + q + out) /
+  algorithmic bytes per launch (decode KV bytes + prefill K/V + q + out, and
+  with a bf16 pool the folded KV write: new rows read + slots written) /
   average launch duration (HIP events around the launch on its stream; a
   spin kernel queued ahead keeps host launch latency out of the interval, and
   consecutive launches rotate over the 4 pool copies so the KV is read from
@@ -105,14 +109,18 @@ def main():
         kc, vc, ks, vs = pools[i % nsets]
         return forward_mixed(q, k, v, kc, vc, ctx, w.scale, store_kvcache, ks, vs, phases=phases)
 
-    def attn_only(i, phases):
+    # The step's own launch: with a bf16 pool forward_mixed folds the KV write
+    # into the attention launch (fold=True); the split per-phase launches run
+    # without it, as the reference's per-phase calls do.
+    def attn_only(i, phases, fold=False):
         kc, vc, ks, vs = pools[i % nsets]
+        store = dict(store_slot_mapping=slots, new_k=k, new_v=v) if fold else {}
         return paged_attention(
             q, kc, vc, w.scale, num_kv_heads=8, k_scale=ks, v_scale=vs, num_decode=meta.num_decode,
             decode_lens=meta.decode_lens, decode_tables=meta.decode_tables,
             num_prefill=meta.prefill_cu_q.numel() - 1, prefill_cu_q=meta.prefill_cu_q,
             prefill_cu_k=meta.prefill_cu_k, max_q=meta.max_q, max_k=meta.max_k,
-            prefill_tables=meta.prefill_tables, phases=phases, out=out_buf)
+            prefill_tables=meta.prefill_tables, phases=phases, out=out_buf, **store)
 
     hq, hkv, d = 32, 8, 128
     elem = 1.0 if fp8 else 2.0
@@ -176,7 +184,7 @@ def main():
 
     out_buf = torch.empty_like(q)
     if args.profile:
-        launch = {"fused": lambda i: attn_only(i, _lib.PHASE_ALL), "decode": lambda i: attn_only(i, _lib.PHASE_DECODE),
+        launch = {"fused": lambda i: attn_only(i, _lib.PHASE_ALL, not fp8), "decode": lambda i: attn_only(i, _lib.PHASE_DECODE),
                   "prefill": lambda i: attn_only(i, _lib.PHASE_PREFILL), "qk": qk_launch,
                   "lm_head": lm_launch}[args.profile]
         src = torch.empty(256 << 20, dtype=torch.uint8, device=device)
@@ -216,7 +224,7 @@ def main():
     value = tokens * steps / elapsed
 
     # ---- per-launch kernel durations (HIP events on the launch stream, cold cache)
-    def launch_times(phases):
+    def launch_times(phases, fold=False):
         stream = torch.cuda.current_stream()
         times = []
         for i in range(args.events + args.warmup):
@@ -224,14 +232,14 @@ def main():
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            attn_only(i, phases)
+            attn_only(i, phases, fold)
             e1.record(stream)
             e1.synchronize()
             if i >= args.warmup:
                 times.append(e0.elapsed_time(e1) * 1e3)  # us
         return statistics.mean(times), statistics.median(times)
 
-    t_fused, t_fused_med = launch_times(_lib.PHASE_ALL)
+    t_fused, t_fused_med = launch_times(_lib.PHASE_ALL, not fp8)
     t_dec, t_dec_med = launch_times(_lib.PHASE_DECODE)
     t_pre, t_pre_med = launch_times(_lib.PHASE_PREFILL)
 
@@ -239,7 +247,9 @@ def main():
     pre_kv_tokens = sum(n + p for n, p in zip(w.prefill_q, w.prefill_prefix))
     pre_bytes = pre_kv_tokens * hkv * (2 * d * elem + 2 * scale_b)
     qo_bytes = 2 * tokens * hq * d * 2
-    fused_bytes = dec_bytes + pre_bytes + qo_bytes
+    # the KV write folded into the bf16 launch: new K/V rows read, pool slots written
+    store_bytes = 0 if fp8 else 2 * tokens * hkv * d * 2 * 2
+    fused_bytes = dec_bytes + pre_bytes + qo_bytes + store_bytes
     flops = w.prefill_flops()
     fused_gbs = fused_bytes / (t_fused * 1e-6) / 1e9
     dec_gbs = (dec_bytes + 2 * w.num_decode * hq * d * 2) / (t_dec * 1e-6) / 1e9
@@ -285,12 +295,14 @@ def main():
             "workload": w.name, "decode_rows": w.num_decode, "decode_context_sum": sum(w.decode_lens),
             "prefill_chunks": w.prefill_q, "prefill_prefixes": w.prefill_prefix, "new_tokens": tokens,
             "heads": [hq, hkv, d], "block_size": w.block_size, "kv_cache": args.kv,
-            "step": "store_kvcache + one fused ragged attention launch", "pool_copies_rotated": nsets,
+            "step": ("store_kvcache + one fused ragged attention launch" if fp8 else
+                     "one fused ragged attention launch with the KV write folded in (forward_mixed)"),
+            "pool_copies_rotated": nsets,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(fused_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(fused_gbs / HBM_PEAK_GBS, 4), "traffic": traffic("fused"),
-            "kernel": "paged_attention_kernel (fused decode+prefill)",
+            "kernel": "paged_attention_kernel (fused decode+prefill" + ("" if fp8 else ", KV write folded in") + ")",
             "algorithmic_bytes_per_launch": fused_bytes, "avg_launch_us": round(t_fused, 2),
             "median_launch_us": round(t_fused_med, 2),
         },

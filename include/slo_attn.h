@@ -190,6 +190,27 @@ typedef struct slo_paged_attention_args {
   void* workspace;                /* zero-filled once at allocation */
   size_t workspace_bytes;
   int32_t phases;                 /* SLO_PHASE_* mask */
+
+  /* Optional KV write in the same launch (bf16 pools only), the store of
+   * forward_mixed / Attention.forward (nanovllm/layers/mixed_attention.py:
+   * 33, nanovllm/layers/attention.py:66-67) folded into the attention
+   * launch.  When store_slot_mapping is not NULL, new row t of new_k/new_v
+   * ([num_new_rows == num_q_rows, num_kv_heads, head_dim] bf16 rows, 16-byte
+   * aligned, row strides multiples of 8: decode rows' tokens first,
+   * then the prefill rows' tokens in cu_seqlens_q order) is written to pool
+   * slot store_slot_mapping[t] (slots < 0 or past the pool are skipped), and
+   * the launch reads the step's new tokens from new_k/new_v instead of the
+   * pool: token decode_lens[b] - 1 of decode row b is new row b, and key j >=
+   * Lk - Lq of a prefill row read through prefill_tables is new row
+   * num_decode + cu_q[r] + j - (Lk - Lq).  The result equals the separate
+   * store followed by this launch, bit for bit; no slot written by the launch
+   * may be read through a table by it except as such a new token. */
+  const int32_t* store_slot_mapping;  /* [num_new_rows] or NULL */
+  const void* new_k;
+  int64_t new_k_row_stride;
+  const void* new_v;
+  int64_t new_v_row_stride;
+  int32_t num_new_rows;
 } slo_paged_attention_args;
 
 /*

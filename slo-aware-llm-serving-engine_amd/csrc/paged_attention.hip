@@ -133,6 +133,17 @@ struct Params {
   // the phases) start at q_off_prefill + cu_q_all[np_all]; they get zeros.
   const int32_t* cu_q_all;
   int32_t np_all;
+  // KV write of the step's new tokens in this launch (bf16 pools; sslots is
+  // null otherwise): new row t goes to slot sslots[t], and the launch reads
+  // the new tokens from nk/nv (decode row b: row b; key j >= prefix of a
+  // prefill row read through its table: its query row's index).
+  const int32_t* sslots;
+  const uint16_t* nk;
+  const uint16_t* nv;
+  int64_t nk_stride;
+  int64_t nv_stride;
+  int32_t nnew;
+  int64_t num_slots;
 };
 
 // The two tile stages live in two separate __shared__ arrays of STAGE_BYTES
@@ -524,7 +535,7 @@ __device__ __forceinline__ void decode_issue_q(const Params& p, uint8_t* qbuf, c
 // from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN: K codes (128 B
 // rows, chunk c in slot c ^ (r & 7)) at 0, V codes likewise at 2048, K scales
 // at 4096 and V scales at 4160.
-template <bool FP8>
+template <bool FP8, bool FOLD>
 __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, const DMeta& m, int s, int wave,
                                              int lane) {
   const int n = lane & 15, g = lane >> 4;
@@ -547,15 +558,20 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
     const uint16_t* kc = static_cast<const uint16_t*>(p.k_cache) + base;
     const uint16_t* vc = static_cast<const uint16_t*>(p.v_cache) + base;
     const uint32_t dst = lds_addr(stg);
+    // With the KV write in this launch, the row's newest token (its last) is
+    // read from the new rows: its slot is written by this same launch.
+    const int tnew = FOLD ? decode_L(p, m) - 1 - t0 : -1;  // its row in this step, if any
+    const uint16_t* kn = FOLD ? p.nk + (int64_t)m.b * p.nk_stride + m.h * HD : kc;
+    const uint16_t* vn = FOLD ? p.nv + (int64_t)m.b * p.nv_stride + m.h * HD : vc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(kc + r * row + 8 * (n ^ (r & 15)), dst + i * 1024);
+      dma16((r == tnew ? kn : kc + r * row) + 8 * (n ^ (r & 15)), dst + i * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + g;
-      dma16(vc + r * row + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
+      dma16((r == tnew ? vn : vc + r * row) + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
     }
   } else {
     const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
@@ -795,20 +811,33 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
   if (tid == 0) atomicExch(&p.counters[b * p.hkv + h], 0);
 }
 
-// Split-K merge tasks, one per (decode row, kv head) in row-major order, are
-// spread over the work lists (task t on list t % nlist) and taken from each
-// list's own counter by that list's workgroups once their items are done.  A
+// Tail tasks, taken by each workgroup once its items are done: first the KV
+// write of the launch's new tokens (when the launch carries it), then the
+// split-K merges.  Store task i of list l writes new rows [4g, 4g + 4) for
+// g = l + i * nlist: each K and V row is copied to its slot (slots < 0 or
+// past the pool are skipped).  Nothing in the launch reads those slots (the
+// new tokens are read from the new rows), so the writes need no ordering and
+// the workgroups that finish their items first do them.  Merge tasks, one per
+// (decode row, kv head) in row-major order, are spread over the work lists
+// (task t on list t % nlist) and taken from each list's own counter.  A merge
 // task waits until all chunk tickets of its (row, head) have arrived (each
 // chunk increments the ticket only after its partial stores are complete, and
-// the chunks are processed by running workgroups that never wait on merge
+// the chunks are processed by running workgroups that never wait on tail
 // tasks), merges, and resets the ticket for the next launch.  Like the work
 // lists, a counter starts at zero: a launch makes exactly tasks + workgroups
 // fetches on it, and the workgroup making the last one resets it.
-__device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
+constexpr int STORE_ROWS = 4;  // new rows per store task
+template <bool STORE>
+__device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
   uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (2 * NLIST + list) * CTRL_STRIDE;
+  const int ngroups = STORE ? (p.nnew + STORE_ROWS - 1) / STORE_ROWS : 0;
+  const uint32_t nstore = list < ngroups ? (uint32_t)((ngroups - list + nlist - 1) / nlist) : 0u;
   const int ntask = p.nd * p.hkv;
-  const uint32_t count = list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u;
+  const uint32_t count = nstore + (list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u);
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
+  if (count == 0) return;  // a list without tasks is not touched: its counter stays zero
+  const int row = p.hkv * HD;            // elements of one K (or V) row
+  const int pieces = STORE_ROWS * 2 * (row / 8);  // 16-byte pieces of one store task
   for (;;) {
     if (tid == 0) sm.item = atomicAdd(mctr, 1u);
     lds_sync();
@@ -818,7 +847,36 @@ __device__ void merge_tasks(const Params& p, Smem& sm, int list, int nlist, int 
       if (tid == 0 && rel == count + wgs - 1u) __hip_atomic_store(mctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    const int task = list + (int)rel * nlist;
+    if (STORE && rel < nstore) {
+      // Copy rows [4g, 4g + 4): all loads of the task first, then the stores.
+      const int t0 = STORE_ROWS * (list + (int)rel * nlist);
+      for (int i0 = 0; i0 < pieces; i0 += 4 * NT) {
+        u32x4 x[4];
+        int64_t dst[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = i0 + tid + j * NT;
+          const int t = t0 + i / (2 * (row / 8)), pc = i % (2 * (row / 8));
+          const bool isv = pc >= row / 8;
+          const int e = 8 * (isv ? pc - row / 8 : pc);
+          dst[j] = -1;
+          x[j] = u32x4{0, 0, 0, 0};
+          if (i < pieces && t < p.nnew) {
+            const int64_t slot = p.sslots[t];
+            x[j] = ld16((isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + e);
+            if (slot >= 0 && slot < p.num_slots) dst[j] = 2 * (slot * row + e) + (isv ? 1 : 0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (dst[j] < 0) continue;
+          uint16_t* base = static_cast<uint16_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
+          *reinterpret_cast<u32x4*>(base + (dst[j] >> 1)) = x[j];
+        }
+      }
+      continue;
+    }
+    const int task = list + (int)(rel - nstore) * nlist;
     const int b = task / p.hkv, h = task % p.hkv;
     const int L = min(max(p.dlens[b], 0), p.dtab_width * p.block_size);
     const int nch = max(1, (L + dchunk - 1) / dchunk);
@@ -871,7 +929,7 @@ __device__ __forceinline__ void wait_vm(int extra) {
 // nxt is learned at step 1 from the fetch issued at the end of the previous
 // item, so a workgroup holds at most its current item and one claimed item
 // that has not started.
-template <bool FP8>
+template <bool FP8, bool FOLD>
 __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
                            uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
                            int r0, int dchunk, int tid) {
@@ -894,10 +952,10 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   lds_sync();
   decode_meta_read(cur, sm, 0);
   decode_issue_q(p, qbuf, cur, wave, lane);
-  decode_issue<FP8>(p, sa, cur, 0, wave, lane);
+  decode_issue<FP8, FOLD>(p, sa, cur, 0, wave, lane);
   for (int i = 0; i < hgp; ++i)
     if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
-  decode_issue<FP8>(p, sb, cur, 1, wave, lane);
+  decode_issue<FP8, FOLD>(p, sb, cur, 1, wave, lane);
   uint32_t f = 0;
   bool fetching = true;  // the fetch in flight is a real one
   if (tid == 0) f = atomic_add_ret(ctr, 1u);
@@ -922,7 +980,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
     float m = NEG_INF, l = 0.0f;
     decode_step<FP8>(p, sa, decode_ntok(p, cur, 0, wave), qv, o, m, l, lane);
-    decode_issue<FP8>(p, sa, cur, 2, wave, lane);
+    decode_issue<FP8, FOLD>(p, sa, cur, 2, wave, lane);
 
     // Step 1: (cur, 1) has landed, and with it prev's stores (every
     // wavefront's, after the barrier) and the fetch.  Wavefront 0 finds the
@@ -952,7 +1010,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       decode_meta_dma(p, sm, nxt, (k + 1) & 1, lane);
     }
     decode_step<FP8>(p, sb, decode_ntok(p, cur, 1, wave), qv, o, m, l, lane);
-    decode_issue<FP8>(p, sb, cur, 3, wave, lane);
+    decode_issue<FP8, FOLD>(p, sb, cur, 3, wave, lane);
 
     // Step 2: (cur, 2) and nxt's metadata have landed; the broadcast is
     // visible after the barrier.
@@ -971,14 +1029,14 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     if (!has1) nxt = cur;  // no next item: its loads repeat the current item's
     decode_issue_q(p, qnxt, nxt, wave, lane);
     if (!half) decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
-    decode_issue<FP8>(p, sa, nxt, 0, wave, lane);
+    decode_issue<FP8, FOLD>(p, sa, nxt, 0, wave, lane);
 
     // Step 3: (cur, 3) has landed.
     wait_vm<GROUP + 1>(0);
     if (!half) decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
-    decode_issue<FP8>(p, sb, nxt, 1, wave, lane);
+    decode_issue<FP8, FOLD>(p, sb, nxt, 1, wave, lane);
     fetching = fetching && has1;
     if (tid == 0) f = atomic_add_ret(ctr, fetching ? 1u : 0u);
     prev = cur;
@@ -993,7 +1051,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // --------------------------------------------------------------- prefill item
-template <bool FP8, int NQT>
+template <bool FP8, int NQT, bool FOLD>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
   constexpr int BQ = 16 * NQT;
   const int lane = tid & 63, wave = tid >> 6;
@@ -1104,6 +1162,27 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     // which buffer a DMA writes); the loop waits for them explicitly.
     const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
     const uint32_t vdst = kdst + TILE_BYTES;
+    if (FOLD && paged && kv0 + TT > prefix) {
+      // With the KV write in this launch, keys from the prefix on are the
+      // row's new tokens, read from the new rows (key j: new row qrow0 + j -
+      // prefix); their slots are written by this same launch.
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int row = (tid >> 4) + 16 * it;
+        const int j = kv0 + row;
+        if (row < nv) {
+          const int ksw = kgo[it] - row * krow, vsw = vgo[it] - row * vrow;  // swizzled chunk offsets
+          const int64_t t = min(qrow0 + j - prefix, (int64_t)p.nnew - 1);
+          const bool nw = j >= prefix;
+          dma16(nw ? p.nk + t * p.nk_stride + (int64_t)h * HD + ksw : ksrc + kgo[it], kdst + 16 * it * ROWB);
+          dma16(nw ? p.nv + t * p.nv_stride + (int64_t)h * HD + vsw : vsrc + vgo[it], vdst + 16 * it * ROWB);
+        } else {
+          st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
+          st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
+        }
+      }
+      return;
+    }
     if (nv == TT) {  // full tile: DMA only
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
@@ -1273,7 +1352,11 @@ enum Mode : int {
   MODE_DECODE = 2,   // decode rows only
 };
 
-template <bool FP8, int MODE>
+// FOLD: the launch carries the KV write of the step's new tokens (bf16
+// pools): prefill tiles read new tokens from the new rows, and the tail tasks
+// include the store.  A separate instantiation, so launches without it keep
+// the prefill tile loop's smaller register footprint.
+template <bool FP8, int MODE, bool FOLD = false>
 __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   constexpr bool HAS_DEC = MODE != MODE_PREFILL;
   constexpr bool HAS_PF = MODE != MODE_DECODE;
@@ -1474,13 +1557,15 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       if (HAS_PF && r < p.np) {
         const int item = list + (int)rel * nlist;
         if constexpr (MODE == MODE_PREFILL) {
-          if (bq == 16) prefill_item<FP8, 1>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-          else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
         } else if constexpr (HAS_PF) {
           int wr = 0, tr = 0;
           if constexpr (FP8) pf_work(p, r, wr, tr);
-          if (FP8 && tr > sm.split_tiles) prefill_item<FP8, FP8 ? 1 : 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-          else prefill_item<FP8, 2>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          if (FP8 && tr > sm.split_tiles)
+            prefill_item<FP8, FP8 ? 1 : 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          else
+            prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
         }
         // The next item is fetched only now: fetching ahead would let a
         // workgroup claim a second item before a late-starting one takes its
@@ -1493,14 +1578,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       }
       // The rest of this decode list is one streaming decode run.
       if constexpr (HAS_DEC)
-        decode_run<FP8>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r,
+        decode_run<FP8, FOLD>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r,
                         dchunk, ltid);
       break;
     }
     if (tid == 0 && sm.item == count + wgs - 1u) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
-  if constexpr (HAS_DEC) merge_tasks(p, sm, list, nlist, decode_base, dchunk, tid);
+  tail_tasks<FOLD>(p, sm, list, nlist, decode_base, dchunk, tid);
 
   // Rows that belong to no decode or prefill row (the capacity padding of a
   // captured step) get zeros, so every output row is defined.
@@ -1609,6 +1694,17 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
         return fail(SLO_ERR_INVALID, "paged_attention: contiguous K/V must be 16-byte aligned bf16 rows");
     }
   }
+  const bool store = a->store_slot_mapping != nullptr;
+  if (store) {
+    if (fp8) return fail(SLO_ERR_UNSUPPORTED, "paged_attention: the KV write in the launch needs a bf16 pool");
+    if (!a->k_cache || !a->v_cache || a->num_blocks <= 0 || a->block_size <= 0)
+      return fail(SLO_ERR_INVALID, "paged_attention: the KV write needs the pool");
+    const int64_t row = (int64_t)a->num_kv_heads * HD;
+    if (!a->new_k || !a->new_v || a->num_new_rows != a->num_q_rows || a->new_k_row_stride < row ||
+        a->new_v_row_stride < row || (a->new_k_row_stride % 8) || (a->new_v_row_stride % 8) ||
+        (reinterpret_cast<uintptr_t>(a->new_k) % 16) || (reinterpret_cast<uintptr_t>(a->new_v) % 16))
+      return fail(SLO_ERR_INVALID, "paged_attention: new K/V must be 16-byte aligned bf16 rows, one per query row");
+  }
   // Workspace: control words, split-K tickets, then decode partials.
   size_t need = 0;
   const int dec_len_cap = do_dec ? a->decode_table_width * a->block_size : 0;
@@ -1658,6 +1754,13 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   p.ctrl = reinterpret_cast<int*>(ws);
   p.counters = reinterpret_cast<int*>(ws + CTRL_BYTES);
   p.partials = reinterpret_cast<float*>(ws + PARTIALS_OFFSET);
+  p.sslots = store ? a->store_slot_mapping : nullptr;
+  p.nk = static_cast<const uint16_t*>(a->new_k);
+  p.nv = static_cast<const uint16_t*>(a->new_v);
+  p.nk_stride = a->new_k_row_stride;
+  p.nv_stride = a->new_v_row_stride;
+  p.nnew = store ? a->num_new_rows : 0;
+  p.num_slots = (int64_t)a->num_blocks * a->block_size;
   p.cu_q_all = a->num_prefill > 0 ? a->prefill_cu_q : nullptr;
   p.np_all = a->num_prefill > 0 && a->prefill_cu_q ? a->num_prefill : 0;
 
@@ -1676,6 +1779,14 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
+  if (store) {  // bf16 pool (checked above)
+    switch (mode) {
+      case MODE_MIXED: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED, true>), dim3(grid), dim3(NT), 0, s, p); break;
+      case MODE_PREFILL: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL, true>), dim3(grid), dim3(NT), 0, s, p); break;
+      default: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_DECODE, true>), dim3(grid), dim3(NT), 0, s, p); break;
+    }
+    return check_launch("paged_attention");
+  }
   switch (mode + 3 * (fp8_reads ? 1 : 0)) {
     case 0: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
     case 1: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;

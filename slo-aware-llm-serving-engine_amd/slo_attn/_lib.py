@@ -52,6 +52,10 @@ class PagedAttentionArgs(ctypes.Structure):
         ("softmax_scale", ctypes.c_float),
         ("workspace", _c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("phases", _c_int32),
+        ("store_slot_mapping", _c_void_p),
+        ("new_k", _c_void_p), ("new_k_row_stride", _c_int64),
+        ("new_v", _c_void_p), ("new_v_row_stride", _c_int64),
+        ("num_new_rows", _c_int32),
     ]
 
 

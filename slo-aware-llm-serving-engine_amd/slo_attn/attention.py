@@ -23,7 +23,7 @@ from torch import nn
 
 from .context import get_context
 from .mixed_attention import forward_mixed
-from .ops import paged_attention, store_kvcache
+from .ops import check_store, paged_attention, store_kvcache
 
 __all__ = ["Attention", "store_kvcache"]
 
@@ -53,20 +53,27 @@ class Attention(nn.Module):
             return forward_mixed(q, k, v, k_cache, v_cache, context, self.scale,
                                  _stored if kv_stored else store_kvcache, self.k_scale, self.v_scale)
         have_cache = bool(k_cache.numel() and v_cache.numel())
-        if have_cache and not kv_stored:
+        # A bf16 pool is written inside the attention launch (same result, one
+        # launch less); an E4M3FN pool by the store kernel first.
+        fold = have_cache and not kv_stored and self.k_scale is None
+        if fold:
+            check_store(k, v, k_cache, v_cache, context.slot_mapping)
+        elif have_cache and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping, *self._scales())
+        store = dict(store_slot_mapping=context.slot_mapping, new_k=k, new_v=v) if fold else {}
         if context.is_prefill:
             rows = context.cu_seqlens_q.numel() - 1
             paged = context.block_tables is not None
+            pool = paged or fold
             return paged_attention(
-                q, k_cache if paged else None, v_cache if paged else None, self.scale,
+                q, k_cache if pool else None, v_cache if pool else None, self.scale,
                 num_kv_heads=self.num_kv_heads, k_scale=self.k_scale if paged else None,
                 v_scale=self.v_scale if paged else None, num_prefill=rows,
                 prefill_cu_q=context.cu_seqlens_q, prefill_cu_k=context.cu_seqlens_k,
                 max_q=context.max_seqlen_q, max_k=context.max_seqlen_k,
-                prefill_tables=context.block_tables, k=None if paged else k, v=None if paged else v)
+                prefill_tables=context.block_tables, k=None if paged else k, v=None if paged else v, **store)
         o = paged_attention(
             q, k_cache, v_cache, self.scale, num_kv_heads=self.num_kv_heads,
             k_scale=self.k_scale, v_scale=self.v_scale, num_decode=q.shape[0],
-            decode_lens=context.context_lens, decode_tables=context.block_tables)
+            decode_lens=context.context_lens, decode_tables=context.block_tables, **store)
         return o.unsqueeze(1)

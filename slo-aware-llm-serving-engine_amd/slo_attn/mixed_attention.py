@@ -14,7 +14,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .ops import paged_attention
+from .ops import check_store, paged_attention, store_kvcache
 
 
 @dataclass
@@ -44,7 +44,12 @@ def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
     meta = context.mixed
     if not k_cache.numel() or not v_cache.numel():
         raise RuntimeError("mixed forward requires an allocated KV pool")
-    if k_scale is None:
+    # The library's own store into a bf16 pool runs inside the attention
+    # launch (same result, one launch less); any other store_fn runs first.
+    fold = store_fn is store_kvcache and k_scale is None and phases == _lib.PHASE_ALL
+    if fold:
+        check_store(k, v, k_cache, v_cache, context.slot_mapping)
+    elif k_scale is None:
         store_fn(k, v, k_cache, v_cache, context.slot_mapping)
     else:
         store_fn(k, v, k_cache, v_cache, context.slot_mapping, k_scale, v_scale)
@@ -59,4 +64,6 @@ def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
         num_prefill=num_prefill, prefill_cu_q=meta.prefill_cu_q, prefill_cu_k=meta.prefill_cu_k,
         max_q=meta.max_q, max_k=meta.max_k,
         prefill_tables=meta.prefill_tables if history else None,
-        k=None if history else k[d:], v=None if history else v[d:], phases=phases)
+        k=None if history else k[d:], v=None if history else v[d:], phases=phases,
+        store_slot_mapping=context.slot_mapping if fold else None, new_k=k if fold else None,
+        new_v=v if fold else None)

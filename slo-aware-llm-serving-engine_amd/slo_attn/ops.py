@@ -57,18 +57,9 @@ def _int32(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------ KV write
-def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
-                  v_cache: torch.Tensor, slot_mapping: torch.Tensor,
-                  k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
-                  scale_floor: float = _lib.FP8_SCALE_FLOOR) -> None:
-    """Slot-mapped KV write (nanovllm/layers/attention.py:33-40), bf16 or E4M3FN.
-
-    ``key``/``value``: ``[N, num_kv_heads, head_dim]`` bf16 whose rows may be
-    strided (a view of the fused QKV output).  ``k_cache``/``v_cache``:
-    ``[num_blocks, block_size, num_kv_heads, head_dim]``; for E4M3FN caches
-    (uint8 or float8_e4m3fn) ``k_scale``/``v_scale`` are the fp32
-    ``[num_blocks, block_size, num_kv_heads]`` scale pools.
-    """
+def check_store(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scale=None):
+    """The store's argument checks (nanovllm/layers/attention.py:36-39 and the
+    formats); returns ``(device, kv_dtype code)``."""
     N, num_heads, head_dim = key.shape
     D = num_heads * head_dim
     # Same stride contract as the reference store (attention.py:36-39).
@@ -94,6 +85,24 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
             if s.dtype != torch.float32 or not s.is_contiguous() or s.numel() != num_slots * num_heads:
                 raise ValueError("scale pools must be contiguous fp32 [num_blocks, block_size, num_kv_heads]")
     _int32(slot_mapping, "slot_mapping")
+    return device, code
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                  k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+                  scale_floor: float = _lib.FP8_SCALE_FLOOR) -> None:
+    """Slot-mapped KV write (nanovllm/layers/attention.py:33-40), bf16 or E4M3FN.
+
+    ``key``/``value``: ``[N, num_kv_heads, head_dim]`` bf16 whose rows may be
+    strided (a view of the fused QKV output).  ``k_cache``/``v_cache``:
+    ``[num_blocks, block_size, num_kv_heads, head_dim]``; for E4M3FN caches
+    (uint8 or float8_e4m3fn) ``k_scale``/``v_scale`` are the fp32
+    ``[num_blocks, block_size, num_kv_heads]`` scale pools.
+    """
+    device, code = check_store(key, value, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+    N, num_heads, head_dim = key.shape
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
     lib = _lib.load()
     _lib.check(lib.slo_store_kvcache(
         _ptr(key), key.stride(0), _ptr(value), value.stride(0), _ptr(slot_mapping), N, num_heads,
@@ -258,7 +267,9 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
                     prefill_cu_k: torch.Tensor | None = None, max_q: int = 0, max_k: int = 0,
                     prefill_tables: torch.Tensor | None = None,
                     k: torch.Tensor | None = None, v: torch.Tensor | None = None,
-                    phases: int = _lib.PHASE_ALL, out: torch.Tensor | None = None) -> torch.Tensor:
+                    phases: int = _lib.PHASE_ALL, out: torch.Tensor | None = None,
+                    store_slot_mapping: torch.Tensor | None = None, new_k: torch.Tensor | None = None,
+                    new_v: torch.Tensor | None = None) -> torch.Tensor:
     """One ragged launch: decode rows ``q[:num_decode]``, then prefill rows.
 
     Decode row b attends to ``decode_lens[b]`` cached tokens through
@@ -267,6 +278,12 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
     aligned, to ``cu_k[r+1]-cu_k[r]`` keys from the pool (``prefill_tables``)
     or, with ``prefill_tables=None``, from the contiguous ``k``/``v`` rows
     starting at ``cu_k[r]``.  Returns ``out`` ``[q rows, num_heads, head_dim]``.
+
+    With ``store_slot_mapping`` (bf16 pools), the same launch also writes
+    ``new_k``/``new_v`` (one row per query row: decode tokens, then prefill
+    tokens) to their slots, the store of forward_mixed folded in, and reads the
+    step's new tokens from those rows; the result is the separate store
+    followed by the launch, bit for bit.
     """
     if q.dim() != 3:
         raise ValueError("q must be [tokens, num_heads, head_dim]")
@@ -337,6 +354,18 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
             args.k, args.k_row_stride = k.data_ptr(), k.stride(0)
             args.v, args.v_row_stride = v.data_ptr(), v.stride(0)
             args.num_kv_rows = min(k.shape[0], v.shape[0])
+    if store_slot_mapping is not None:
+        check_store(new_k, new_v, k_cache, v_cache, store_slot_mapping)
+        if code != _lib.KV_BF16:
+            raise ValueError("the KV write in the attention launch needs a bf16 pool")
+        if new_k.shape[0] != T or new_k.shape[1] != num_kv_heads or new_k.shape[2] != head_dim:
+            raise ValueError("new_k/new_v must hold one [num_kv_heads, head_dim] row per query row")
+        args.k_cache, args.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        args.num_blocks, args.block_size = k_cache.shape[0], k_cache.shape[1]
+        args.store_slot_mapping = store_slot_mapping.data_ptr()
+        args.new_k, args.new_k_row_stride = new_k.data_ptr(), new_k.stride(0)
+        args.new_v, args.new_v_row_stride = new_v.data_ptr(), new_v.stride(0)
+        args.num_new_rows = T
     args.num_heads, args.num_kv_heads, args.head_dim = num_heads, num_kv_heads, head_dim
     args.softmax_scale = float(softmax_scale)
     args.phases = int(phases)

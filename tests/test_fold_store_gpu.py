@@ -1,0 +1,146 @@
+"""The KV write folded into the attention launch (bf16 pools).
+
+``forward_mixed`` and ``Attention.forward`` run the library's own store inside
+the attention launch: the launch writes the step's new K/V rows to their slots
+and reads the new tokens from those rows instead of the pool.  The reference
+order is store first, then attend (nanovllm/layers/mixed_attention.py:33-34,
+nanovllm/layers/attention.py:66-67); these tests check that the folded launch
+gives the same output and the same pool bytes, bit for bit, as that order run
+as two launches (a ``store_fn`` that is not the library's own store takes the
+two-launch path), on the benchmark workloads (decode rows, prefill rows with
+and without history) and through the V0 branches, including slot -1 padding.
+"""
+import pytest
+import torch
+
+from slo_attn import (Attention, MixedAttentionContext, forward_mixed, reserve_workspace, reset_context,
+                      set_context, store_kvcache, workloads)
+from slo_attn.ops import paged_attention
+from types import SimpleNamespace
+
+pytestmark = pytest.mark.gpu
+
+
+def _two_launch_store(*args):
+    store_kvcache(*args)
+
+
+@pytest.mark.parametrize("index", [0, 1, 2, 3])
+def test_forward_mixed_folded_store_equals_store_then_attend(device, index):
+    w = workloads.config(index)
+    d = workloads.to_device(w, device)
+    ctx = SimpleNamespace(mixed=d["meta"], slot_mapping=d["slot_mapping"])
+    q, k, v = d["q"], d["k"], d["v"]
+    kc0, vc0 = w.k_cache.to(device), w.v_cache.to(device)
+    if w.num_decode:
+        reserve_workspace(device, w.num_decode, max(len(t) for t in w.decode_tables) * w.block_size, 32, 8, 128)
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    ref = forward_mixed(q, k, v, kc0, vc0, ctx, w.scale, _two_launch_store)
+    got = forward_mixed(q, k, v, kc1, vc1, ctx, w.scale, store_kvcache)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16))
+
+
+def test_folded_store_skips_padding_slots_and_matches_explicit_launch(device):
+    # Decode rows of a captured batch: real rows, then padding rows (slot -1,
+    # length 0).  The folded launch must leave every byte but the real slots
+    # alone and give the outputs of store + attend.
+    g = torch.Generator().manual_seed(9)
+    hq, hkv, dh, bs, nblk = 32, 8, 128, 256, 6
+    pool_k = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    pool_v = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    lens = [300, 1, 257, 0, 0]
+    tables = torch.tensor([[0, 1, -1], [2, -1, -1], [3, 4, -1], [-1, -1, -1], [5, 5, 5]],
+                          dtype=torch.int32, device=device)
+    slots = torch.tensor([bs + 43, 2 * bs, 4 * bs + 0, -1, -1], dtype=torch.int32, device=device)
+    B = len(lens)
+    q = torch.randn(B, hq, dh, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(B, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(B, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    dl = torch.tensor(lens, dtype=torch.int32, device=device)
+    reserve_workspace(device, B, 3 * bs, hq, hkv, dh)
+    kc0, vc0 = pool_k.clone(), pool_v.clone()
+    store_kvcache(k, v, kc0, vc0, slots)
+    ref = paged_attention(q, kc0, vc0, dh ** -0.5, num_kv_heads=hkv, num_decode=B, decode_lens=dl,
+                          decode_tables=tables)
+    kc1, vc1 = pool_k.clone(), pool_v.clone()
+    got = paged_attention(q, kc1, vc1, dh ** -0.5, num_kv_heads=hkv, num_decode=B, decode_lens=dl,
+                          decode_tables=tables, store_slot_mapping=slots, new_k=k, new_v=v)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16))
+
+
+def test_v0_branches_fold_the_store(device):
+    # Cold prefill, prefix-cache prefill and decode through Attention.forward
+    # (bf16 pool: folded) against the same calls with the store run first and
+    # kv_stored=True (two launches).
+    g = torch.Generator().manual_seed(11)
+    hq, hkv, dh, bs, nblk = 32, 8, 128, 256, 8
+    a1 = Attention(hq, dh, dh ** -0.5, hkv)
+    a2 = Attention(hq, dh, dh ** -0.5, hkv)
+    base_k = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    base_v = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    a1.k_cache, a1.v_cache = base_k.clone(), base_v.clone()
+    a2.k_cache, a2.v_cache = base_k.clone(), base_v.clone()
+
+    def i32(x):
+        return torch.tensor(x, dtype=torch.int32, device=device)
+
+    def both(q, k, v, **ctx):
+        set_context(**ctx)
+        try:
+            got = a1(q, k, v)
+            store_kvcache(k, v, a2.k_cache, a2.v_cache, ctx["slot_mapping"])
+            ref = a2(q, k, v, kv_stored=True)
+        finally:
+            reset_context()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(a1.k_cache.view(torch.int16), a2.k_cache.view(torch.int16))
+        assert torch.equal(a1.v_cache.view(torch.int16), a2.v_cache.view(torch.int16))
+
+    # cold prefill: two prompts of 100 and 300 tokens in blocks 0 and 1-2
+    lq = [100, 300]
+    T = sum(lq)
+    q = torch.randn(T, hq, dh, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(T, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(T, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    slots = list(range(0, 100)) + list(range(bs, bs + 300))
+    both(q, k, v, is_prefill=True, cu_seqlens_q=i32([0, 100, T]), cu_seqlens_k=i32([0, 100, T]),
+         max_seqlen_q=300, max_seqlen_k=300, slot_mapping=i32(slots))
+    # prefix-cache prefill: row 0 has 256 cached tokens (block 3) + 60 new (block 4)
+    q = torch.randn(60, hq, dh, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(60, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(60, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    both(q, k, v, is_prefill=True, cu_seqlens_q=i32([0, 60]), cu_seqlens_k=i32([0, 316]),
+         max_seqlen_q=60, max_seqlen_k=316, slot_mapping=i32(list(range(4 * bs, 4 * bs + 60))),
+         block_tables=i32([[3, 4]]))
+    # decode: the two prompts' next tokens plus a padded row
+    q = torch.randn(3, hq, dh, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(3, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(3, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    reserve_workspace(device, 3, 2 * bs, hq, hkv, dh)
+    both(q, k, v, is_prefill=False, slot_mapping=i32([100, bs + 300, -1]), context_lens=i32([101, 301, 0]),
+         block_tables=i32([[0, -1], [1, 2], [-1, -1]]))
+
+
+def test_fold_rejects_fp8_pool_and_bad_rows(device):
+    hq, hkv, dh, bs = 8, 2, 128, 256
+    q = torch.zeros(2, hq, dh, dtype=torch.bfloat16, device=device)
+    k = torch.zeros(2, hkv, dh, dtype=torch.bfloat16, device=device)
+    kc = torch.zeros(2, bs, hkv, dh, dtype=torch.uint8, device=device)
+    sc = torch.ones(2, bs, hkv, device=device)
+    dl = torch.tensor([1, 1], dtype=torch.int32, device=device)
+    tb = torch.tensor([[0], [1]], dtype=torch.int32, device=device)
+    slots = torch.tensor([0, bs], dtype=torch.int32, device=device)
+    with pytest.raises(ValueError):
+        paged_attention(q, kc, kc.clone(), 1.0, num_kv_heads=hkv, k_scale=sc, v_scale=sc, num_decode=2,
+                        decode_lens=dl, decode_tables=tb, store_slot_mapping=slots, new_k=k, new_v=k)
+    kb = torch.zeros(2, bs, hkv, dh, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError):
+        paged_attention(q, kb, kb.clone(), 1.0, num_kv_heads=hkv, num_decode=2, decode_lens=dl, decode_tables=tb,
+                        store_slot_mapping=slots[:1].contiguous(), new_k=k[:1], new_v=k[:1])
