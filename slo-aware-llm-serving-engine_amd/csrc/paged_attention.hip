@@ -1134,6 +1134,15 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       kbase = (int64_t)(k_start + kv0) * p.k_stride + (int64_t)h * HD;
       vbase = (int64_t)(k_start + kv0) * p.v_stride + (int64_t)h * HD;
     }
+    // With the KV write in this launch (FOLD, contiguous new rows of the pool's
+    // row length), tiles from the prefix on hold only new tokens: they are read
+    // from the new rows (key j: new row qrow0 + j - prefix), whose slots this
+    // launch writes at its end.  The row offsets are the pool's.  (The tile
+    // that straddles the prefix, if any, was written to the pool by this item
+    // before its first tile.)
+    bool fresh = false;
+    if constexpr (FOLD) fresh = paged && kv0 >= prefix && qrow0 - prefix + kv0 + ntok <= p.nnew;
+    if (fresh) ok = true;
     const int nv = ok ? ntok : 0;
     if (src_fp8) {
 #pragma unroll
@@ -1157,32 +1166,16 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
     const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
     const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
+    if (fresh) {
+      const int64_t t0 = (qrow0 - prefix + kv0) * p.nk_stride + (int64_t)h * HD;
+      ksrc = p.nk + t0;
+      vsrc = p.nv + t0;
+    }
     // Inline-asm DMA: the compiler does not track these loads, so it inserts
     // no wait for them before the current tile's LDS reads (it cannot tell
     // which buffer a DMA writes); the loop waits for them explicitly.
     const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
     const uint32_t vdst = kdst + TILE_BYTES;
-    if (FOLD && paged && kv0 + TT > prefix) {
-      // With the KV write in this launch, keys from the prefix on are the
-      // row's new tokens, read from the new rows (key j: new row qrow0 + j -
-      // prefix); their slots are written by this same launch.
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int row = (tid >> 4) + 16 * it;
-        const int j = kv0 + row;
-        if (row < nv) {
-          const int ksw = kgo[it] - row * krow, vsw = vgo[it] - row * vrow;  // swizzled chunk offsets
-          const int64_t t = min(qrow0 + j - prefix, (int64_t)p.nnew - 1);
-          const bool nw = j >= prefix;
-          dma16(nw ? p.nk + t * p.nk_stride + (int64_t)h * HD + ksw : ksrc + kgo[it], kdst + 16 * it * ROWB);
-          dma16(nw ? p.nv + t * p.nv_stride + (int64_t)h * HD + vsw : vsrc + vgo[it], vdst + 16 * it * ROWB);
-        } else {
-          st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
-          st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
-        }
-      }
-      return;
-    }
     if (nv == TT) {  // full tile: DMA only
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
@@ -1231,6 +1224,29 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   if (cached)
     for (int i = tid; i < npages; i += NT) sm.u.pf.pages[i] = prow[i];
   __syncthreads();
+  if constexpr (FOLD) {
+    // The tile that straddles the prefix reads its keys from the pool, so this
+    // item first writes that tile's new tokens (head h) to their slots itself:
+    // every item reading the tile writes the same bytes before reading them.
+    const int s0 = prefix & ~(TT - 1), s1 = min(kend, s0 + TT);
+    if (paged && (prefix & (TT - 1)) && prefix < s1) {
+      const int n_new = s1 - prefix;  // tokens, each 16 + 16 pieces of 16 bytes (K, V of head h)
+      for (int i = tid; i < 32 * n_new; i += NT) {
+        const int jj = prefix + (i >> 5), pc = i & 15;
+        const bool isv = i & 16;
+        const int64_t t = min(qrow0 + jj - prefix, (int64_t)p.nnew - 1);
+        const int page = cached ? pages[jj / p.block_size] : prow[jj / p.block_size];
+        if (page < 0 || page >= p.num_blocks) continue;
+        const int64_t slot = (int64_t)page * p.block_size + jj % p.block_size;
+        const uint16_t* src = (isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + (int64_t)h * HD + 8 * pc;
+        uint16_t* dst = static_cast<uint16_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) +
+                        slot * p.hkv * HD + (int64_t)h * HD + 8 * pc;
+        *reinterpret_cast<u32x4*>(dst) = ld16(src);
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // written before any DMA of this item reads them
+      __syncthreads();
+    }
+  }
   if (kend > 0) {
     issue_tile(0, 0);
     commit_tile(0);
@@ -1700,10 +1716,11 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
     if (!a->k_cache || !a->v_cache || a->num_blocks <= 0 || a->block_size <= 0)
       return fail(SLO_ERR_INVALID, "paged_attention: the KV write needs the pool");
     const int64_t row = (int64_t)a->num_kv_heads * HD;
-    if (!a->new_k || !a->new_v || a->num_new_rows != a->num_q_rows || a->new_k_row_stride < row ||
-        a->new_v_row_stride < row || (a->new_k_row_stride % 8) || (a->new_v_row_stride % 8) ||
-        (reinterpret_cast<uintptr_t>(a->new_k) % 16) || (reinterpret_cast<uintptr_t>(a->new_v) % 16))
-      return fail(SLO_ERR_INVALID, "paged_attention: new K/V must be 16-byte aligned bf16 rows, one per query row");
+    if (!a->new_k || !a->new_v || a->num_new_rows != a->num_q_rows || a->new_k_row_stride != row ||
+        a->new_v_row_stride != row || (reinterpret_cast<uintptr_t>(a->new_k) % 16) ||
+        (reinterpret_cast<uintptr_t>(a->new_v) % 16))
+      return fail(SLO_ERR_INVALID,
+                  "paged_attention: new K/V must be contiguous 16-byte aligned bf16 rows, one per query row");
   }
   // Workspace: control words, split-K tickets, then decode partials.
   size_t need = 0;

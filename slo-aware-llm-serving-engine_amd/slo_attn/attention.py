@@ -23,7 +23,7 @@ from torch import nn
 
 from .context import get_context
 from .mixed_attention import forward_mixed
-from .ops import check_store, paged_attention, store_kvcache
+from .ops import check_store, foldable, paged_attention, store_kvcache
 
 __all__ = ["Attention", "store_kvcache"]
 
@@ -53,9 +53,10 @@ class Attention(nn.Module):
             return forward_mixed(q, k, v, k_cache, v_cache, context, self.scale,
                                  _stored if kv_stored else store_kvcache, self.k_scale, self.v_scale)
         have_cache = bool(k_cache.numel() and v_cache.numel())
-        # A bf16 pool is written inside the attention launch (same result, one
-        # launch less); an E4M3FN pool by the store kernel first.
-        fold = have_cache and not kv_stored and self.k_scale is None
+        # A bf16 pool is written inside the attention launch when the new rows
+        # are contiguous (same result, one launch less); otherwise, and for an
+        # E4M3FN pool, the store kernel runs first.
+        fold = have_cache and not kv_stored and self.k_scale is None and foldable(k, v)
         if fold:
             check_store(k, v, k_cache, v_cache, context.slot_mapping)
         elif have_cache and not kv_stored:

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .ops import check_store, paged_attention, store_kvcache
+from .ops import check_store, foldable, paged_attention, store_kvcache
 
 
 @dataclass
@@ -45,8 +45,10 @@ def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
     if not k_cache.numel() or not v_cache.numel():
         raise RuntimeError("mixed forward requires an allocated KV pool")
     # The library's own store into a bf16 pool runs inside the attention
-    # launch (same result, one launch less); any other store_fn runs first.
-    fold = store_fn is store_kvcache and k_scale is None and phases == _lib.PHASE_ALL
+    # launch when the new rows are contiguous (same result, one launch less);
+    # any other store_fn runs first.
+    fold = (store_fn is store_kvcache and k_scale is None and phases == _lib.PHASE_ALL
+            and foldable(k, v))
     if fold:
         check_store(k, v, k_cache, v_cache, context.slot_mapping)
     elif k_scale is None:

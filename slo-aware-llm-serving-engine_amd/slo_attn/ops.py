@@ -88,6 +88,15 @@ def check_store(key, value, k_cache, v_cache, slot_mapping, k_scale=None, v_scal
     return device, code
 
 
+def foldable(key: torch.Tensor, value: torch.Tensor) -> bool:
+    """Whether the attention launch can carry the KV write of these new rows:
+    bf16 ``[N, num_kv_heads, head_dim]`` rows stored back to back."""
+    row = key.shape[1] * key.shape[2]
+    return (key.dim() == 3 and key.dtype == torch.bfloat16 and value.dtype == torch.bfloat16
+            and key.stride(0) == row and value.stride(0) == row and key.stride(2) == 1 and value.stride(2) == 1
+            and key.stride(1) == key.shape[2] and value.stride(1) == value.shape[2])
+
+
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                   v_cache: torch.Tensor, slot_mapping: torch.Tensor,
                   k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,

@@ -144,3 +144,74 @@ def test_fold_rejects_fp8_pool_and_bad_rows(device):
     with pytest.raises(ValueError):
         paged_attention(q, kb, kb.clone(), 1.0, num_kv_heads=hkv, num_decode=2, decode_lens=dl, decode_tables=tb,
                         store_slot_mapping=slots[:1].contiguous(), new_k=k[:1], new_v=k[:1])
+
+
+@pytest.mark.parametrize("prefixes", [(300, 77, 0), (64, 511, 1000)])
+def test_folded_store_with_prefixes_inside_a_key_tile(device, prefixes):
+    # Prefill rows whose cached prefix ends inside a 64-key tile (a chunked
+    # prompt): that tile mixes pool keys and new keys; plus decode rows.  The
+    # folded launch must equal the store followed by the attention launch.
+    g = torch.Generator().manual_seed(13)
+    hq, hkv, dh, bs, nblk = 32, 8, 128, 256, 24
+    pool_k = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    pool_v = torch.randn(nblk, bs, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    perm = torch.randperm(nblk, generator=g).tolist()
+    chunks = [130, 45, 200]
+    dec_lens = [700, 33]
+    rows, tables, slots, nxt = [], [], [], 0
+
+    def take(n_tokens):
+        nonlocal nxt
+        nb = (n_tokens + bs - 1) // bs
+        t = perm[nxt:nxt + nb]
+        nxt += nb
+        return t
+
+    dec_tables = []
+    for L in dec_lens:
+        t = take(L)
+        dec_tables.append(t)
+        slots.append(t[(L - 1) // bs] * bs + (L - 1) % bs)
+    pf_tables = []
+    for pfx, n in zip(prefixes, chunks):
+        t = take(pfx + n)
+        pf_tables.append(t)
+        slots += [t[j // bs] * bs + j % bs for j in range(pfx, pfx + n)]
+    width = max(len(t) for t in dec_tables + pf_tables)
+
+    def pad(ts):
+        return torch.tensor([t + [-1] * (width - len(t)) for t in ts], dtype=torch.int32, device=device)
+
+    T = len(dec_lens) + sum(chunks)
+    q = torch.randn(T, hq, dh, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(T, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(T, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    cu_q = [0]
+    cu_k = [0]
+    for pfx, n in zip(prefixes, chunks):
+        cu_q.append(cu_q[-1] + n)
+        cu_k.append(cu_k[-1] + pfx + n)
+    meta = MixedAttentionContext(len(dec_lens), sum(chunks), torch.tensor(dec_lens, dtype=torch.int32, device=device),
+                                 pad(dec_tables), torch.tensor(cu_q, dtype=torch.int32, device=device),
+                                 torch.tensor(cu_k, dtype=torch.int32, device=device), pad(pf_tables), max(chunks),
+                                 max(p + n for p, n in zip(prefixes, chunks)), True)
+    ctx = SimpleNamespace(mixed=meta, slot_mapping=torch.tensor(slots, dtype=torch.int32, device=device))
+    reserve_workspace(device, len(dec_lens), width * bs, hq, hkv, dh)
+    kc0, vc0 = pool_k.clone(), pool_v.clone()
+    kc1, vc1 = pool_k.clone(), pool_v.clone()
+    ref = forward_mixed(q, k, v, kc0, vc0, ctx, dh ** -0.5, _two_launch_store)
+    got = forward_mixed(q, k, v, kc1, vc1, ctx, dh ** -0.5, store_kvcache)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16))
+    # strided new rows (a view of a fused projection) take the two-launch path
+    wide = torch.randn(T, 3, hkv, dh, generator=g).to(torch.bfloat16).to(device)
+    ks, vs = wide[:, 1], wide[:, 2]
+    kc2, vc2 = pool_k.clone(), pool_v.clone()
+    kc3, vc3 = pool_k.clone(), pool_v.clone()
+    ref2 = forward_mixed(q, ks, vs, kc2, vc2, ctx, dh ** -0.5, _two_launch_store)
+    got2 = forward_mixed(q, ks, vs, kc3, vc3, ctx, dh ** -0.5, store_kvcache)
+    torch.cuda.synchronize()
+    assert torch.equal(got2.view(torch.int16), ref2.view(torch.int16))
+    assert torch.equal(kc3.view(torch.int16), kc2.view(torch.int16))
