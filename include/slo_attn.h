@@ -195,8 +195,8 @@ typedef struct slo_paged_attention_args {
    * forward_mixed / Attention.forward (nanovllm/layers/mixed_attention.py:
    * 33, nanovllm/layers/attention.py:66-67) folded into the attention
    * launch.  When store_slot_mapping is not NULL, new row t of new_k/new_v
-   * ([num_new_rows == num_q_rows, num_kv_heads, head_dim] bf16 rows, 16-byte
-   * aligned, row strides multiples of 8: decode rows' tokens first,
+   * ([num_new_rows == num_q_rows, num_kv_heads, head_dim] bf16, contiguous:
+   * row stride num_kv_heads * head_dim, 16-byte aligned; decode rows' tokens first,
    * then the prefill rows' tokens in cu_seqlens_q order) is written to pool
    * slot store_slot_mapping[t] (slots < 0 or past the pool are skipped), and
    * the launch reads the step's new tokens from new_k/new_v instead of the
