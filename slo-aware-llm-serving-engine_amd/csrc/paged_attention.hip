@@ -2,7 +2,10 @@
 //
 // Replaces the per-phase flash-attn calls of forward_mixed
 // (nanovllm/layers/mixed_attention.py:36-57) and of the V0 branches of
-// Attention.forward (nanovllm/layers/attention.py:68-78).
+// Attention.forward (nanovllm/layers/attention.py:68-78), and, with a bf16
+// pool, the KV write that precedes them (attention.py:10-40): the launch then
+// reads the step's new tokens from their rows and writes them to the pool as
+// tail work (FOLD instantiations).
 //
 // Work list.  Every workgroup (4 wavefronts, two workgroups per CU) first
 // derives, from the metadata alone, the number of work items of every row and
@@ -20,7 +23,8 @@
 //    wavefront owns one of the G query heads that share kv head h, for the
 //    same positions, so the K/V tiles staged in LDS serve all G heads.  The
 //    block size is chosen per launch: 16 when the heaviest row's items would
-//    otherwise outlast the balanced share of a workgroup, else 32.  Tiles
+//    otherwise outlast the balanced share of a workgroup, else 32 (E4M3FN
+//    mixed launches also pick 16 per row for their longest rows).  Tiles
 //    of 64 keys are double-buffered: the next tile's global loads are in
 //    flight while the current one is consumed.  The contraction runs on bf16
 //    MFMA (v_mfma_f32_16x16x32_bf16) in the transposed form S^T = K Q^T,
@@ -34,9 +38,10 @@
 //    go from HBM straight into LDS (global_load_lds) and two steps stay in
 //    flight per wavefront across item boundaries.  The 4 wavefronts merge in
 //    LDS; a row with several chunks writes one (acc, m, l) record per chunk,
-//    and after its own items every workgroup takes split-K merge tasks from
-//    its list, each waiting for the chunks of
-//    its (row, head) (the split-K merge of docs/project_manual.md:643-650).
+//    and after its own items every workgroup takes tail tasks from its list:
+//    the folded KV write's store tasks, then split-K merge tasks, each waiting
+//    for the chunks of its (row, head) (the split-K merge of
+//    docs/project_manual.md:643-650).
 //
 // LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
 // XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 2*(row & 7)), so the MFMA
