@@ -178,6 +178,7 @@ struct Smem {
   int row;
   int salt;
   int split_tiles;  // E4M3FN mixed launches: rows with a heavier 32-position block use 16
+  int pf_first;     // workgroups that start with the prefill family
   int meta[2][8];   // decode: landed row length and block-table entries, by item parity
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
@@ -1463,6 +1464,19 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     // more than the shorter items gain.)
     if (tid == 0)
       sm.split_tiles = (FP8 && MODE == MODE_MIXED) ? (int)((4 * dt * p.hkv + wt) / gridDim.x) : (1 << 30);
+    // Mixed launches: the share of workgroups that start with prefill items
+    // follows the prefill share of the work (decode items counted as 4 tiles),
+    // twice it, between a quarter and five eighths of the grid.  (Five eighths
+    // measured best with a third of the work in prefill, a quarter with a
+    // tenth.)
+    if (tid == 0) {
+      int64_t permille = 500;
+      if (MODE == MODE_MIXED) {
+        const int64_t all = wt + 4 * dt * p.hkv;
+        if (all > 0) permille = min((int64_t)625, max((int64_t)250, 2000 * wt / all));
+      }
+      sm.pf_first = (int)((int64_t)gridDim.x * permille / 1000);
+    }
     __syncthreads();
   }
 
@@ -1511,12 +1525,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // then.  Fetches that add 0 (decode loop padding) may follow the reset;
   // their results are ignored.  No counter is contended by a completion count.
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
-  // Family taken first (0 prefill, 1 decode): the first half of the grid
-  // starts with prefill, the second with decode.  The dispatcher fills every
-  // CU's first workgroup slot before any second one, so workgroups b and
-  // b + grid/2 share a CU and each CU pairs an MFMA-bound prefill workgroup
-  // with an HBM-bound decode one.
-  const int first = 2 * (int)blockIdx.x >= (int)gridDim.x ? 1 : 0;
+  // Family taken first (0 prefill, 1 decode): workgroups below pf_first (a
+  // quarter to five eighths of the grid) start with prefill, the rest with
+  // decode.
+  // The dispatcher fills every CU's first workgroup slot before any second
+  // one, so with a half the workgroups b and b + grid/2 share a CU and each CU
+  // pairs an MFMA-bound prefill workgroup with an HBM-bound decode one.
+  const int pf_first = sm.pf_first;  // workgroups that start with the prefill family
+  const int first = (int)blockIdx.x >= pf_first ? 1 : 0;
   // Static first items: the workgroups of a list that start with a family
   // (all of them when the list has items in one family only) take that
   // family's first items by their index, without a fetch; fetched relative
@@ -1524,8 +1540,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // family is fetched count - S + wgs times per launch (one out-of-list fetch
   // per workgroup).
   const int member = blockIdx.x / nlist;  // index of this workgroup in its list
-  const int half_grid = gridDim.x / 2;
-  const int wfirst0 = half_grid > list ? (half_grid - list + nlist - 1) / nlist : 0;  // prefill-first members
+  const int wfirst0 = pf_first > list ? (pf_first - list + nlist - 1) / nlist : 0;  // prefill-first members
   uint32_t fcount[2];
 #pragma unroll
   for (int fam = 0; fam < 2; ++fam) {
