@@ -821,9 +821,11 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // write of the launch's new tokens (when the launch carries it), then the
 // split-K merges.  Store task i of list l writes new rows [4g, 4g + 4) for
 // g = l + i * nlist: each K and V row is copied to its slot (slots < 0 or
-// past the pool are skipped).  Nothing in the launch reads those slots (the
-// new tokens are read from the new rows), so the writes need no ordering and
-// the workgroups that finish their items first do them.  Merge tasks, one per
+// past the pool are skipped).  Nothing in the launch reads those slots before
+// writing them (the new tokens are read from the new rows; a prefill item
+// whose prefix ends inside a key tile first writes that tile's new tokens
+// itself, the same bytes), so the writes need no ordering and the workgroups
+// that finish their items first do them.  Merge tasks, one per
 // (decode row, kv head) in row-major order, are spread over the work lists
 // (task t on list t % nlist) and taken from each list's own counter.  A merge
 // task waits until all chunk tickets of its (row, head) have arrived (each
