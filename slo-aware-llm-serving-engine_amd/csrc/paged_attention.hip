@@ -96,6 +96,12 @@ constexpr int SPIN_LIMIT = 1 << 22;
 constexpr int MAX_COUNTERS = 65536;
 constexpr int PREC = HD + 4;      // floats per query head in a split-K record: acc[HD], m, l, 2 pad
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
+// Prefill-only launches may split their longest rows' items in two key
+// ranges; each split item writes a record of its 4 wavefronts' (O, m, l) at
+// the start of the partials area (unused by decode there), within this many
+// bytes, which every workspace reserves beyond the decode partials.
+constexpr size_t PF_SPLIT_BYTES = 48u << 20;
+constexpr int PF_REC_FLOATS = 4 * (8 * 64 * 4 + 64 * 2);  // per item and 16 query positions
 constexpr float NEG_INF = -__builtin_huge_valf();
 
 struct Params {
@@ -180,6 +186,8 @@ struct Smem {
   int split_tiles;  // E4M3FN mixed launches: rows with a heavier 32-position block use 16
   int pf_first;     // workgroups that start with the prefill family
   int drot;         // decode items rotate kv heads across chunks (long decode launches)
+  int pf_split_thr; // prefill-only launches: rows with a heavier block split their keys in two
+  int pf_ticket;    // prefill split item: ticket value before this item's arrival
   int meta[2][8];   // decode: landed row length and block-table entries, by item parity
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
@@ -1064,15 +1072,24 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // --------------------------------------------------------------- prefill item
-template <bool FP8, int NQT, bool FOLD>
-__device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid) {
+// SPLITK (prefill-only launches): with `split`, the row's items come in
+// pairs that cover the first and the second half of each block's key tiles
+// (local index ((block * 2 + part) * hkv + h) * HG + hg, global `item`); each
+// writes (O, m, l) of its range as a record, and the one that arrives second
+// on the pair's ticket merges both and writes the output.
+template <bool FP8, int NQT, bool FOLD, bool SPLITK = false>
+__device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid,
+                             int item = 0, bool split = false) {
   constexpr int BQ = 16 * NQT;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
+  const bool two = SPLITK && split;
   const int hg = local % p.HG;
   const int t = local / p.HG;
   const int h = t % p.hkv;
-  const int qb_rev = t / p.hkv;
+  const int u = t / p.hkv;
+  const int part = two ? u & 1 : 0;
+  const int qb_rev = two ? u >> 1 : u;
 
   const PfRow geo = pf_row(p, r);
   const int q_start = geo.q_start, Lq = geo.Lq, k_start = geo.k_start, Lk = geo.Lk;
@@ -1083,6 +1100,11 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   const int q0 = (nqb - 1 - qb_rev) * BQ;  // heaviest blocks are pulled first
   const int qend = min(q0 + BQ, Lq);
   const int kend = min(Lk, max(0, prefix + qend));
+  // Key range of this item: all tiles, or one half (the first half takes the
+  // extra tile of an odd count; the second holds the causal boundary).
+  const int tcut = (kend + 2 * TT - 1) / (2 * TT);
+  const int kstart = two && part ? tcut * TT : 0;
+  const int kstop = two && !part ? min(kend, tcut * TT) : kend;
   const int hl = hg * 4 + wave;
   const bool active = hl < p.G;
   const int hq = h * p.G + hl;
@@ -1260,8 +1282,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       __syncthreads();
     }
   }
-  if (kend > 0) {
-    issue_tile(0, 0);
+  if (kstart < kstop) {
+    issue_tile(kstart, 0);
     commit_tile(0);
   }
   // Each tile is processed as two halves of 32 keys,
@@ -1278,7 +1300,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     const int ntok = min(TT, kend - kv0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     lds_sync();
-    const bool more = kv0 + TT < kend;
+    const bool more = kv0 + TT < kstop;
     const uint8_t* kt = buf ? st1 : st0;
     const uint8_t* vt = kt + TILE_BYTES;
     // K fragment jj of half h: rows 16*(2h + (jj & 1)) + n, k-step jj >> 1.
@@ -1351,9 +1373,66 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // block's first query position (bottom-right causal) need no mask.
   const int lim_first = min(kend - TT, q0 + prefix - (TT - 1));  // largest unmasked kv0
   const int n_int = lim_first < 0 ? 0 : lim_first / TT + 1;
-  int kv0 = 0, j = 0;
-  for (; kv0 < kend && j < n_int; kv0 += TT, ++j) tile(std::integral_constant<bool, false>(), kv0, j);
-  for (; kv0 < kend; kv0 += TT, ++j) tile(std::integral_constant<bool, true>(), kv0, j);
+  const int tfirst = kstart / TT;
+  int kv0 = kstart, j = 0;
+  for (; kv0 < kstop && tfirst + j < n_int; kv0 += TT, ++j) tile(std::integral_constant<bool, false>(), kv0, j);
+  for (; kv0 < kstop; kv0 += TT, ++j) tile(std::integral_constant<bool, true>(), kv0, j);
+
+  if constexpr (SPLITK) {
+    if (two) {
+      // Record layout (floats, NQT * PF_REC_FLOATS per item): O as
+      // [wave][nt][dt][lane] f32x4, then (m, l) as [wave][nt][lane] float2.
+      constexpr int ML = 4 * NQT * 8 * 256;
+      float* rec = p.partials + (size_t)item * (PF_REC_FLOATS * NQT);
+      if (active) {
+#pragma unroll
+        for (int nt = 0; nt < NQT; ++nt) {
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt)
+            store16_agent(rec + (((wave * NQT + nt) * 8 + dt) * 64 + lane) * 4,
+                          __builtin_bit_cast(u32x4, o[dt][nt]));
+          store8_agent(rec + ML + ((wave * NQT + nt) * 64 + lane) * 2,
+                       u32x2{__float_as_uint(m[nt]), __float_as_uint(l[nt])});
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // records stored before the ticket
+      __syncthreads();
+      const int pair = p.hkv * p.HG;
+      int* ticket = &p.counters[item - part * pair];
+      if (tid == 0) {
+        const uint32_t old = atomic_add_ret(ticket, 1u);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        sm.pf_ticket = (int)after_wait(old);
+      }
+      __syncthreads();
+      if (sm.pf_ticket == 0) return;  // the partner item merges
+      if (tid == 0) atomicExch(ticket, 0);
+      if (!active) return;
+      const float* prec = p.partials + (size_t)(part ? item - pair : item + pair) * (PF_REC_FLOATS * NQT);
+      // Merged in a fixed order (first half, then second), so the result's
+      // rounding does not depend on which item arrived second.
+      const float c = p.scale_log2;
+#pragma unroll
+      for (int nt = 0; nt < NQT; ++nt) {
+        const float2 ml = load_partial2(prec + ML + ((wave * NQT + nt) * 64 + lane) * 2);
+        const float m0 = part ? ml.x : m[nt], m1 = part ? m[nt] : ml.x;
+        const float l0 = part ? ml.y : l[nt], l1 = part ? l[nt] : ml.y;
+        const float mx = fmaxf(m0, m1);
+        const float w0 = m0 == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(c * (m0 - mx));
+        const float w1 = m1 == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(c * (m1 - mx));
+        l[nt] = fmaf(l1, w1, l0 * w0);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const float* po = prec + (((wave * NQT + nt) * 8 + dt) * 64 + lane) * 4;
+          const float2 a = load_partial2(po), b = load_partial2(po + 2);
+          const f32x4 pv = f32x4{a.x, a.y, b.x, b.y};
+          const f32x4 o0 = part ? pv : o[dt][nt], o1 = part ? o[dt][nt] : pv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[dt][nt][i] = fmaf(o1[i], w1, o0[i] * w0);
+        }
+      }
+    }
+  }
 
   if (!active) return;
 #pragma unroll
@@ -1490,6 +1569,40 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // short launches (about three items per workgroup) ran 3% slower
       // with it.
       sm.drot = dt * p.hkv >= 6 * (int64_t)gridDim.x;
+      sm.pf_split_thr = MODE == MODE_PREFILL ? (int)max((int64_t)16, 2 * wt / gridDim.x) : (1 << 30);
+    }
+    __syncthreads();
+  }
+
+  // Prefill-only launches: a row whose heaviest block spans more key tiles
+  // than twice a workgroup's share of the work (and at least 16) is split in
+  // two key ranges per item, merged by the range that finishes second, when
+  // every item of the launch has a record slot (a ticket and PF_SPLIT_BYTES
+  // of records); such a row otherwise sets the launch's length alone.
+  if constexpr (MODE == MODE_PREFILL) {
+    int base_c = 0, extra_c = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i >= per || r0 + i >= nrows) continue;
+      const int c = bq == 16 ? cnt_b[i] : cnt_a[i];
+      base_c += c;
+      if (tmr[i] > sm.pf_split_thr) extra_c += c;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      base_c += __shfl_xor(base_c, d, 64);
+      extra_c += __shfl_xor(extra_c, d, 64);
+    }
+    if (lane == 0) {
+      sm.wsum[wave] = base_c;
+      sm.dsum[wave] = extra_c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int all = sm.wsum[0] + sm.wsum[1] + sm.wsum[2] + sm.wsum[3];
+      const int ext = sm.dsum[0] + sm.dsum[1] + sm.dsum[2] + sm.dsum[3];
+      const int cap = (int)(PF_SPLIT_BYTES / (sizeof(float) * (size_t)PF_REC_FLOATS * (bq / 16)));
+      if (ext == 0 || all + ext > cap || all + ext > MAX_COUNTERS) sm.pf_split_thr = 1 << 30;
     }
     __syncthreads();
   }
@@ -1501,6 +1614,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   for (int i = 0; i < 4; ++i) {
     const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == CHUNK_MIN;
     cnt[i] = alt ? cnt_b[i] : cnt_a[i];
+    if (MODE == MODE_PREFILL && r0 + i < p.np && tmr[i] > sm.pf_split_thr) cnt[i] *= 2;
     local_sum += cnt[i];
   }
   int incl = local_sum;
@@ -1607,8 +1721,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       if (HAS_PF && r < p.np) {
         const int item = list + (int)rel * nlist;
         if constexpr (MODE == MODE_PREFILL) {
-          if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          bool sp = false;
+          {
+            int wr = 0, tr = 0;
+            pf_work(p, r, wr, tr);
+            sp = tr > sm.pf_split_thr;
+          }
+          if (bq == 16) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, sp);
+          else prefill_item<FP8, 2, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, sp);
         } else if constexpr (HAS_PF) {
           int wr = 0, tr = 0;
           if constexpr (FP8) pf_work(p, r, wr, tr);
@@ -1694,7 +1814,7 @@ extern "C" int slo_attention_workspace_bytes(int32_t max_decode_rows, int32_t ma
   if (head_dim != HD) return fail(SLO_ERR_UNSUPPORTED, "workspace_bytes: head_dim must be 128");
   const int64_t chunks = (max_decode_len + CHUNK_MIN - 1) / CHUNK_MIN;
   const int64_t items = (int64_t)max_decode_rows * std::max<int64_t>(1, chunks) * num_kv_heads;
-  *bytes = PARTIALS_OFFSET + sizeof(float) * partial_floats(items, num_heads / num_kv_heads);
+  *bytes = PARTIALS_OFFSET + sizeof(float) * partial_floats(items, num_heads / num_kv_heads) + PF_SPLIT_BYTES;
   return SLO_OK;
 }
 

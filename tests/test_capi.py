@@ -41,7 +41,8 @@ def test_workspace_bytes_and_errors():
     # one record of G x (128 accumulators + m + l + 2 pad) floats per chunk of at least 128 tokens
     per_item = 4 * (128 + 4) * 4
     assert n2 - n1 == 24 * (4096 // 128) * 8 * per_item
-    assert n0 == 24 * 128 + 1024 + 4 * 65536
+    # control words, 65536 tickets and 48 MiB of split prefill records
+    assert n0 == 24 * 128 + 1024 + 4 * 65536 + (48 << 20)
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.workspace_bytes(1, 1, 32, 8, 64)
     with pytest.raises(RuntimeError):
