@@ -366,6 +366,15 @@ __device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& 
 __device__ __forceinline__ void store_partial(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Prefill-only launches split a row's items in two key ranges when its
+// heaviest block spans more than `thr` key tiles and its cached prefix is at
+// least as long as its chunk (measured: splitting cold rows made a launch of
+// four 1.1k-token rows 5% slower, while rows after long prefixes gained).
+__device__ __forceinline__ bool pf_splits(const Params& p, int r, int tiles, int thr) {
+  if (tiles <= thr) return false;
+  const PfRow g = pf_row(p, r);
+  return g.prefix >= g.Lq;
+}
 __device__ __forceinline__ float load_partial(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1575,7 +1584,8 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   }
 
   // Prefill-only launches: a row whose heaviest block spans more key tiles
-  // than twice a workgroup's share of the work (and at least 16) is split in
+  // than twice a workgroup's share of the work (and at least 16), after a
+  // cached prefix at least as long as its chunk, is split in
   // two key ranges per item, merged by the range that finishes second, when
   // every item of the launch has a record slot (a ticket and PF_SPLIT_BYTES
   // of records); such a row otherwise sets the launch's length alone.
@@ -1586,7 +1596,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       if (i >= per || r0 + i >= nrows) continue;
       const int c = bq == 16 ? cnt_b[i] : cnt_a[i];
       base_c += c;
-      if (tmr[i] > sm.pf_split_thr) extra_c += c;
+      if (pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) extra_c += c;
     }
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -1614,7 +1624,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   for (int i = 0; i < 4; ++i) {
     const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == CHUNK_MIN;
     cnt[i] = alt ? cnt_b[i] : cnt_a[i];
-    if (MODE == MODE_PREFILL && r0 + i < p.np && tmr[i] > sm.pf_split_thr) cnt[i] *= 2;
+    if (MODE == MODE_PREFILL && r0 + i < p.np && pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) cnt[i] *= 2;
     local_sum += cnt[i];
   }
   int incl = local_sum;
@@ -1725,10 +1735,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
           {
             int wr = 0, tr = 0;
             pf_work(p, r, wr, tr);
-            sp = tr > sm.pf_split_thr;
+            sp = pf_splits(p, r, tr, sm.pf_split_thr);
           }
-          if (bq == 16) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, sp);
-          else prefill_item<FP8, 2, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, sp);
+          // Split items only where the row splits (which implies 16-position
+          // blocks); other items keep the tile loop compiled without the
+          // split's range and merge code.
+          if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, true);
+          else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
         } else if constexpr (HAS_PF) {
           int wr = 0, tr = 0;
           if constexpr (FP8) pf_work(p, r, wr, tr);

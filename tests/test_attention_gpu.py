@@ -147,14 +147,14 @@ def test_gqa_ratios(device, hq, hkv):
 @pytest.mark.parametrize("phases", [2, 3])
 def test_prefill_rows_split_in_key_halves(device, kv_fp8, phases):
     # prefill-only launches: the rows whose heaviest block spans more key
-    # tiles than twice a workgroup's share (and at least 16) run as pairs of
-    # items over the two halves of each block's keys, merged by the second.
-    # First case: two long-prefix rows split beside unsplit lighter rows.
-    # Second: one 1,100-token row over an 8-token prefix alone, split, whose
-    # first blocks have an empty second half (one key tile) or a second half
-    # in which some queries see no key (72 keys: queries 48..55 end before 64).
+    # tiles than twice a workgroup's share (and at least 16), after a cached
+    # prefix at least as long as their chunk, run as pairs of items over the
+    # two halves of each block's keys, merged by the second.  First case: two
+    # long-prefix rows split beside unsplit lighter and cold rows (odd tile
+    # counts: 4096 + 512 keys end mid-tile for the 16-position blocks).
+    # Second: one row of 1,100 new tokens after 1,100 cached ones, alone.
     cases = (Case([], [4096, 0, 2900, 1, 130], [512, 700, 96, 33, 5], seed=12, kv_fp8=kv_fp8),
-             Case([], [8], [1100], seed=13, kv_fp8=kv_fp8))
+             Case([], [1100], [1100], seed=13, kv_fp8=kv_fp8))
     for case in cases:
         (mx, mn), got, _ = _check(case, device, phases)
         print(f"split prefill fp8={kv_fp8} phases={phases}: max-abs {mx:.3e} mean-abs {mn:.3e}")
