@@ -33,7 +33,8 @@ enum {
   SLO_ERR_INVALID = 1,     /* bad argument, shape or stride */
   SLO_ERR_HIP = 2,         /* a HIP runtime call failed */
   SLO_ERR_WORKSPACE = 3,   /* workspace smaller than slo_attention_workspace_bytes */
-  SLO_ERR_UNSUPPORTED = 4  /* geometry this build does not implement */
+  SLO_ERR_UNSUPPORTED = 4, /* geometry this build does not implement */
+  SLO_ERR_STATE = 5        /* a workspace word that must be zero between launches is not */
 };
 
 enum { SLO_KV_BF16 = 0, SLO_KV_FP8_E4M3FN = 1 };
@@ -230,10 +231,36 @@ int slo_attention_workspace_bytes(int32_t max_decode_rows, int32_t max_decode_le
  * (nanovllm/layers/attention.py:75-78) and the V0 prefill call
  * (nanovllm/layers/attention.py:68-74).  The work list (split-K decode chunks
  * and prefill query tiles) is built on the GPU from the metadata, and split-K
- * partials are merged inside the same launch.  Launches that share one
- * workspace must be ordered on one stream.
+ * partials are merged inside the same launch.  The grid is the number of
+ * workgroups of the launched kernel the GPU holds at once, so a merge's chunks
+ * are computed while it waits; should they not arrive within the bounded wait
+ * (see slo_attention_workspace_check) the merge gives up and the event is
+ * counted.  Every work-list counter and ticket of the workspace is zero again
+ * when the launch ends.  Launches that share one workspace must be ordered on
+ * one stream.
  */
 int slo_paged_attention(const slo_paged_attention_args* args, slo_stream_t stream);
+
+/*
+ * Diagnostic, not for the hot path: waits for `stream`, then checks the state
+ * every slo_paged_attention launch leaves in `workspace`: every work-list
+ * counter and split-K ticket zero, and no split-K merge that gave up waiting.
+ * (A merge task waits at most 200 ms, or SLO_ATTN_MERGE_WAIT_US microseconds,
+ * for the chunks of its (row, kv head); chunks come from workgroups of the same
+ * launch, which are all resident unless another kernel holds the GPU's compute
+ * units.  A task that gives up writes nothing for its rows and counts the
+ * event; the tickets still return to zero, so later launches are unaffected.)
+ * Returns SLO_OK, or SLO_ERR_STATE naming a nonzero word (the workspace must
+ * then be zero-filled before its next launch) or the number of merges that
+ * gave up since the last check (their decode outputs are invalid).  When
+ * `events` is not NULL it receives the 4 event counters, [0] merges that gave
+ * up, [1] split prefill item pairs merged, [2..3] zero; the counters are
+ * cleared, so each event is reported once.  It synchronises, so it refuses a
+ * stream under capture.  No counterpart in the reference (flash-attn keeps no
+ * state between calls): it backs the contract of slo_paged_attention.
+ */
+int slo_attention_workspace_check(const void* workspace, size_t workspace_bytes, uint32_t* events,
+                                  slo_stream_t stream);
 
 /* Description of the last error on the calling thread ("" if none). */
 const char* slo_last_error(void);

@@ -37,11 +37,13 @@
 //    wavefront; the G query heads sharing h are the MFMA columns.  K, V and Q
 //    go from HBM straight into LDS (global_load_lds) and two steps stay in
 //    flight per wavefront across item boundaries.  The 4 wavefronts merge in
-//    LDS; a row with several chunks writes one (acc, m, l) record per chunk,
-//    and after its own items every workgroup takes tail tasks from its list:
-//    the folded KV write's store tasks, then split-K merge tasks, each waiting
-//    for the chunks of its (row, head) (the split-K merge of
-//    docs/project_manual.md:643-650).
+//    LDS; a row with several chunks writes one (acc, m, l) record per chunk
+//    and increments the (row, kv head) ticket; the workgroup whose increment
+//    completes the count merges the records (the split-K merge of
+//    docs/project_manual.md:643-650) once its own items are done.  No
+//    workgroup ever waits for another, so the launch is correct whatever the
+//    number of workgroups resident at once.  After their items, workgroups
+//    take the folded KV write's store tasks from their list.
 //
 // LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
 // XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 2*(row & 7)), so the MFMA
@@ -62,6 +64,10 @@
 // which is the dequantise-then-attend definition with the scale applied in
 // fp32.
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
 #include <mutex>
 #include "common.h"
 #include "capi_internal.h"
@@ -81,18 +87,22 @@ constexpr int MAX_G = 16;              // query heads per kv head
 constexpr int MAX_PAGES = 256;         // prefill block-table entries cached in LDS
 constexpr int NLIST = 8;          // work lists (one per XCD)
 constexpr int CTRL_STRIDE = 32;   // uint32 words between lists: one 128-byte line each
-// Control words: one line per prefill work list, per decode work list and per
-// split-K merge-task list.
-// Control area: three families of NLIST list lines (prefill, decode, merge
-// tasks), then a trash line that decode wavefronts without a query head store
-// to, so every wavefront issues the same number of stores per item.
+// Control area (4 KiB): three families of NLIST list lines (prefill items,
+// decode items, tail tasks), one 128-byte line each, then a 1 KiB line whose
+// first 528 bytes are the trash that decode wavefronts without a query head
+// store to (so every wavefront issues the same number of stores per item)
+// and whose last 128 bytes hold event counters (EV_*) that only the host's
+// diagnostic reads and clears.  Every word of the list lines is zero between
+// launches.
 constexpr int TRASH_OFFSET = 3 * NLIST * CTRL_STRIDE * 4;
 constexpr int TRASH_BYTES = 1024;
+constexpr int EVENTS_OFFSET = TRASH_OFFSET + TRASH_BYTES - 128;
 constexpr int CTRL_BYTES = TRASH_OFFSET + TRASH_BYTES;
-// Word of the control area set to 1 when a split-K merge gave up waiting
-// (SPIN_LIMIT sleeps, about 0.2 s); it is never cleared by the kernel.
-constexpr int FAULT_WORD = 2 * NLIST * CTRL_STRIDE + 2;
-constexpr int SPIN_LIMIT = 1 << 22;
+enum : int {
+  EV_MERGE_GAVE_UP = 0,   // split-K merge tasks that stopped waiting (their outputs are not written)
+  EV_PF_SPLIT_MERGE = 1,  // split prefill item pairs merged by their second item
+  EV_COUNT = 4,
+};
 constexpr int MAX_COUNTERS = 65536;
 constexpr int PREC = HD + 4;      // floats per query head in a split-K record: acc[HD], m, l, 2 pad
 constexpr size_t PARTIALS_OFFSET = CTRL_BYTES + sizeof(int) * (size_t)MAX_COUNTERS;
@@ -155,6 +165,9 @@ struct Params {
   int64_t nv_stride;
   int32_t nnew;
   int64_t num_slots;
+  // How long a split-K merge task waits for its chunks before it gives up
+  // (s_memrealtime ticks).
+  int64_t merge_wait_ticks;
 };
 
 // The two tile stages live in two separate __shared__ arrays of STAGE_BYTES
@@ -404,6 +417,11 @@ __device__ __forceinline__ float load_partial(const float* p) {
 // block-table entries into LDS and broadcasts the row; the fetch and ticket
 // results are read after a wait that covers them, through an empty asm that
 // ties the value to that point.
+//
+// Split-K: an item of a row with several chunks stores its record, and once
+// the stores of every wavefront are acknowledged (the wait and barrier of the
+// next item's step 1) wavefront 0 adds 1 to the (row, kv head) ticket; the
+// merge is a tail task (tail_tasks).
 constexpr int DT = 16;                 // tokens per wavefront step
 constexpr int DSTEP = 4 * DT;          // tokens per workgroup step
 constexpr int NSTEP = CHUNK / DSTEP;   // workgroup steps per item
@@ -798,6 +816,8 @@ __device__ __forceinline__ void decode_merge(const Params& p, Smem& sm, uint8_t*
 // Final split-K merge of (row b, kv head h): a thread owns one query head and
 // two adjacent d; the chunks' (m, l) and accumulator pairs are read 16 chunks
 // at a time (agent-scope 8-byte loads), merged online, and the ticket reset.
+// Run once the ticket counts every chunk: every record is stored and
+// acknowledged before its increment, and the loads bypass the per-XCD L2.
 __device__ __forceinline__ float2 load_partial2(const float* p) {
   const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -835,7 +855,9 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
     *reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * G + hn) * HD + d) =
         pack_bf16x2(O0 * inv, O1 * inv);
   }
-  if (tid == 0) atomicExch(&p.counters[b * p.hkv + h], 0);
+  // The launch's nch increments are matched by one decrement of nch: the
+  // ticket is zero for the next launch whatever the order.
+  if (tid == 0) __hip_atomic_fetch_add(&p.counters[b * p.hkv + h], -nch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Tail tasks, taken by each workgroup once its items are done: first the KV
@@ -846,15 +868,19 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // writing them (the new tokens are read from the new rows; a prefill item
 // whose prefix ends inside a key tile first writes that tile's new tokens
 // itself, the same bytes), so the writes need no ordering and the workgroups
-// that finish their items first do them.  Merge tasks, one per
-// (decode row, kv head) in row-major order, are spread over the work lists
-// (task t on list t % nlist) and taken from each list's own counter.  A merge
-// task waits until all chunk tickets of its (row, head) have arrived (each
-// chunk increments the ticket only after its partial stores are complete, and
-// the chunks are processed by running workgroups that never wait on tail
-// tasks), merges, and resets the ticket for the next launch.  Like the work
-// lists, a counter starts at zero: a launch makes exactly tasks + workgroups
-// fetches on it, and the workgroup making the last one resets it.
+// that finish their items first do them.  Merge tasks, one per (decode row,
+// kv head) in row-major order, are spread over the work lists (task t on
+// list t % nlist).  A merge task waits until all chunk tickets of its (row,
+// head) have arrived (each chunk increments the ticket only after its record
+// is stored, and chunks are run by workgroups that are resident: the grid is
+// what the GPU holds of this instantiation at once), merges, and takes nch
+// off the ticket.  The wait is bounded by merge_wait_ticks (200 ms); a task
+// that gives up writes nothing, takes nch off the ticket all the same (the
+// late increments bring it back to zero, so the next launch is unaffected)
+// and counts the event, which slo_attention_workspace_check reports as an
+// error.  Like the work lists, the task counter starts at zero: a launch
+// makes exactly tasks + workgroups fetches on it, and the workgroup making
+// the last one resets it.
 constexpr int STORE_ROWS = 4;  // new rows per store task
 template <bool STORE>
 __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
@@ -865,7 +891,7 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
   const uint32_t count = nstore + (list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u);
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
   if (count == 0) return;  // a list without tasks is not touched: its counter stays zero
-  const int row = p.hkv * HD;            // elements of one K (or V) row
+  const int row = p.hkv * HD;                     // elements of one K (or V) row
   const int pieces = STORE_ROWS * 2 * (row / 8);  // 16-byte pieces of one store task
   for (;;) {
     if (tid == 0) sm.item = atomicAdd(mctr, 1u);
@@ -908,23 +934,35 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
     const int task = list + (int)(rel - nstore) * nlist;
     const int b = task / p.hkv, h = task % p.hkv;
     const int L = min(max(p.dlens[b], 0), p.dtab_width * p.block_size);
-    const int nch = max(1, (L + dchunk - 1) / dchunk);
+    const uint32_t nch = (uint32_t)max(1, (L + dchunk - 1) / dchunk);
     if (nch == 1) continue;
-    int* ticket = &p.counters[b * p.hkv + h];
-    // Bounded wait: a ticket that never completes (an inconsistent workspace)
-    // raises the fault word and lets the launch end instead of hanging.
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(&p.counters[b * p.hkv + h]);
     if (tid == 0) {
-      int spins = 0;
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      bool ok = true;
       while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nch) {
-        if (++spins > SPIN_LIMIT) {
-          store4(p.ctrl + FAULT_WORD, 1u);
+        if ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) > p.merge_wait_ticks) {
+          ok = false;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
       }
+      if (!ok) {
+        // The chunks did not all arrive in time (workgroups of this launch
+        // could not run: the GPU is shared, or the grid exceeds what it
+        // holds).  No merge: the outputs of (b, h) stay unwritten and the
+        // event counter reports it to the host.  The ticket still drops by
+        // nch, so the late increments bring it back to zero.
+        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(p.ctrl) + EVENTS_OFFSET / 4 + EV_MERGE_GAVE_UP, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ticket, 0u - nch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      sm.row = ok ? 1 : 0;
     }
     lds_sync();
-    decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, nch, tid);
+    const bool mine = __builtin_amdgcn_readfirstlane(sm.row) != 0;
+    lds_sync();
+    if (mine) decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, (int)nch, tid);
   }
 }
 
@@ -1415,7 +1453,11 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       }
       __syncthreads();
       if (sm.pf_ticket == 0) return;  // the partner item merges
-      if (tid == 0) atomicExch(ticket, 0);
+      if (tid == 0) {
+        atomicExch(ticket, 0);
+        __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(p.ctrl) + EVENTS_OFFSET / 4 + EV_PF_SPLIT_MERGE, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       if (!active) return;
       const float* prec = p.partials + (size_t)(part ? item - pair : item + pair) * (PF_REC_FLOATS * NQT);
       // Merged in a fixed order (first half, then second), so the result's
@@ -1763,7 +1805,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // The rest of this decode list is one streaming decode run.
       if constexpr (HAS_DEC)
         decode_run<FP8, FOLD>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r,
-                        dchunk, ltid);
+                              dchunk, ltid);
       break;
     }
     if (tid == 0 && sm.item == count + wgs - 1u) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1784,9 +1826,29 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   }
 }
 
+using AttnKernel = void (*)(Params);
+
+// The instantiations, indexed [fold][fp8][mode] (FOLD launches use bf16 pools).
+AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
+  static const AttnKernel table[2][2][3] = {
+      {{paged_attention_kernel<false, MODE_MIXED>, paged_attention_kernel<false, MODE_PREFILL>,
+        paged_attention_kernel<false, MODE_DECODE>},
+       {paged_attention_kernel<true, MODE_MIXED>, paged_attention_kernel<true, MODE_PREFILL>,
+        paged_attention_kernel<true, MODE_DECODE>}},
+      {{paged_attention_kernel<false, MODE_MIXED, true>, paged_attention_kernel<false, MODE_PREFILL, true>,
+        paged_attention_kernel<false, MODE_DECODE, true>},
+       {nullptr, nullptr, nullptr}},
+  };
+  return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
+}
+
+// Compute units and, per instantiation, the workgroups one CU holds at once
+// (registers and LDS of that kernel), cached per device.  A persistent launch
+// of CUs x that many workgroups keeps every workgroup resident.
 struct DeviceShape {
   int cus = 0;
-  int wg_per_cu[2] = {0, 0};
+  int wallclock_khz = 0;  // s_memrealtime rate
+  int wg_per_cu[2][2][3] = {};
 };
 
 int device_shape(DeviceShape* out) {
@@ -1798,15 +1860,20 @@ int device_shape(DeviceShape* out) {
   std::lock_guard<std::mutex> lock(mu);
   if (!ready[dev]) {
     DeviceShape s;
-    if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&s.wallclock_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
       return fail(SLO_ERR_HIP, "hipDeviceGetAttribute failed");
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[0], paged_attention_kernel<false, MODE_MIXED>, NT,
-                                                     0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&s.wg_per_cu[1], paged_attention_kernel<true, MODE_MIXED>, NT,
-                                                     0) != hipSuccess)
-      return fail(SLO_ERR_HIP, "occupancy query failed");
-    s.wg_per_cu[0] = std::max(1, s.wg_per_cu[0]);
-    s.wg_per_cu[1] = std::max(1, s.wg_per_cu[1]);
+    if (s.wallclock_khz <= 0) s.wallclock_khz = 100000;
+    for (int fold = 0; fold < 2; ++fold)
+      for (int fp8 = 0; fp8 < 2; ++fp8)
+        for (int mode = 0; mode < 3; ++mode) {
+          const AttnKernel k = attn_kernel(fold, fp8, mode);
+          if (!k) continue;
+          int n = 0;
+          if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, NT, 0) != hipSuccess)
+            return fail(SLO_ERR_HIP, "occupancy query failed");
+          s.wg_per_cu[fold][fp8][mode] = std::max(1, n);
+        }
     cache[dev] = s;
     ready[dev] = true;
   }
@@ -1946,6 +2013,13 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   p.nv_stride = a->new_v_row_stride;
   p.nnew = store ? a->num_new_rows : 0;
   p.num_slots = (int64_t)a->num_blocks * a->block_size;
+  // A merge task waits up to 200 ms for its chunks (a whole decode launch
+  // takes well under a millisecond) before it gives up and reports it.
+  // SLO_ATTN_MERGE_WAIT_US overrides the bound (0 makes every merge whose
+  // chunks are not all in give up, which the tests use to run that path).
+  int64_t wait_us = 200000;
+  if (const char* e = std::getenv("SLO_ATTN_MERGE_WAIT_US")) wait_us = std::max(0LL, std::atoll(e));
+  p.merge_wait_ticks = wait_us * ds.wallclock_khz / 1000;
   p.cu_q_all = a->num_prefill > 0 ? a->prefill_cu_q : nullptr;
   p.np_all = a->num_prefill > 0 && a->prefill_cu_q ? a->num_prefill : 0;
 
@@ -1960,25 +2034,62 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   // cold prefill rows (new K/V only) runs the bf16 one, which holds fewer
   // registers.
   const bool fp8_reads = fp8 && (do_dec || (do_pf && p.ptab != nullptr));
-  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fp8_reads ? 1 : 0];
-  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
-  if (store) {  // bf16 pool (checked above)
-    switch (mode) {
-      case MODE_MIXED: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED, true>), dim3(grid), dim3(NT), 0, s, p); break;
-      case MODE_PREFILL: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL, true>), dim3(grid), dim3(NT), 0, s, p); break;
-      default: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_DECODE, true>), dim3(grid), dim3(NT), 0, s, p); break;
-    }
-    return check_launch("paged_attention");
-  }
-  switch (mode + 3 * (fp8_reads ? 1 : 0)) {
-    case 0: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
-    case 1: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((paged_attention_kernel<false, MODE_DECODE>), dim3(grid), dim3(NT), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_MIXED>), dim3(grid), dim3(NT), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_PREFILL>), dim3(grid), dim3(NT), 0, s, p); break;
-    default: hipLaunchKernelGGL((paged_attention_kernel<true, MODE_DECODE>), dim3(grid), dim3(NT), 0, s, p); break;
-  }
+  const AttnKernel kernel = attn_kernel(store, fp8_reads, mode);  // store implies a bf16 pool (checked above)
+  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[store ? 1 : 0][fp8_reads ? 1 : 0][mode];
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
+  void* kargs[] = {&p};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid), dim3(NT), kargs, 0,
+                      static_cast<hipStream_t>(stream)) != hipSuccess)
+    return fail(SLO_ERR_HIP, "paged_attention: launch failed");
   return check_launch("paged_attention");
+}
+
+extern "C" int slo_attention_workspace_check(const void* workspace, size_t workspace_bytes, uint32_t* events,
+                                             slo_stream_t stream) {
+  if (!workspace || workspace_bytes < PARTIALS_OFFSET)
+    return fail(SLO_ERR_INVALID, "workspace_check: workspace missing or smaller than its control area");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess) return fail(SLO_ERR_HIP, "workspace_check: hipStreamIsCapturing failed");
+  if (cap != hipStreamCaptureStatusNone) return fail(SLO_ERR_INVALID, "workspace_check: the stream is being captured");
+  if (hipStreamSynchronize(s) != hipSuccess) return fail(SLO_ERR_HIP, "workspace_check: hipStreamSynchronize failed");
+  std::vector<uint32_t> words(PARTIALS_OFFSET / 4);
+  if (hipMemcpy(words.data(), workspace, PARTIALS_OFFSET, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(SLO_ERR_HIP, "workspace_check: hipMemcpy failed");
+  // Event counters: handed out, then cleared, so each event is reported once.
+  uint32_t ev[EV_COUNT];
+  std::memcpy(ev, words.data() + EVENTS_OFFSET / 4, sizeof ev);
+  if (events) std::memcpy(events, ev, sizeof ev);
+  bool any = false;
+  for (int i = 0; i < EV_COUNT; ++i) any = any || ev[i];
+  if (any) {
+    const uint32_t zeros[EV_COUNT] = {};
+    if (hipMemcpy(static_cast<char*>(const_cast<void*>(workspace)) + EVENTS_OFFSET, zeros, sizeof zeros,
+                  hipMemcpyHostToDevice) != hipSuccess)
+      return fail(SLO_ERR_HIP, "workspace_check: hipMemcpy failed");
+  }
+  static const char* const family[3] = {"prefill item", "decode item", "tail task"};
+  for (size_t i = 0; i < words.size(); ++i) {
+    if (i * 4 >= (size_t)TRASH_OFFSET && i * 4 < (size_t)CTRL_BYTES) continue;  // trash and event lines
+    if (!words[i]) continue;
+    char msg[160];
+    if (i * 4 < (size_t)TRASH_OFFSET) {
+      const int line = (int)(i / CTRL_STRIDE);
+      snprintf(msg, sizeof msg, "workspace_check: %s counter of list %d (word %d) is %u, not 0",
+               family[line / NLIST], line % NLIST, (int)(i % CTRL_STRIDE), words[i]);
+    } else {
+      snprintf(msg, sizeof msg, "workspace_check: ticket %zu is %#x, not 0", i - CTRL_BYTES / 4, words[i]);
+    }
+    return fail(SLO_ERR_STATE, msg);
+  }
+  if (ev[EV_MERGE_GAVE_UP]) {
+    char msg[200];
+    snprintf(msg, sizeof msg,
+             "workspace_check: %u split-K merges gave up waiting for their chunks since the last check; those "
+             "decode outputs were not written (workgroups of the launch could not run in time)",
+             ev[EV_MERGE_GAVE_UP]);
+    return fail(SLO_ERR_STATE, msg);
+  }
+  return SLO_OK;
 }

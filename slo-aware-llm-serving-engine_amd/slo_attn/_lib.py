@@ -69,6 +69,7 @@ EXPORTS = (
     "slo_build_mixed_metadata",
     "slo_attention_workspace_bytes",
     "slo_paged_attention",
+    "slo_attention_workspace_check",
     "slo_last_error",
     "slo_paged_attention_args_size",
 )
@@ -109,6 +110,8 @@ def load() -> ctypes.CDLL:
             _c_int32, _c_int32, _c_int32, _c_int32, _c_int32, ctypes.POINTER(ctypes.c_size_t)]
         lib.slo_paged_attention.restype = ctypes.c_int
         lib.slo_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_void_p]
+        lib.slo_attention_workspace_check.restype = ctypes.c_int
+        lib.slo_attention_workspace_check.argtypes = [_c_void_p, ctypes.c_size_t, _c_void_p, _c_void_p]
         lib.slo_last_error.restype = ctypes.c_char_p
         lib.slo_last_error.argtypes = []
         lib.slo_paged_attention_args_size.restype = ctypes.c_size_t

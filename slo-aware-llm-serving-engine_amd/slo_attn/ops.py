@@ -260,6 +260,35 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return ws
 
 
+def check_workspaces() -> None:
+    """Raise if any device's attention workspace is not in the state every
+    launch leaves it in (work-list counters and split-K tickets zero), or if a
+    split-K merge gave up waiting since the last check (its decode outputs were
+    not written).  Synchronises the current stream of each device; call it
+    outside graph capture, e.g. every few hundred steps of a serving loop."""
+    for index, ws in list(_workspaces.items()):
+        device = torch.device("cuda", index)
+        _lib.check(_lib.load().slo_attention_workspace_check(ws.data_ptr(), ws.numel(), None, _stream(device)),
+                   "slo_attention_workspace_check")
+
+
+def workspace_events(device) -> dict:
+    """Reads and clears the attention workspace's event counters on ``device``
+    (after checking its zero invariants): ``merges_gave_up`` (split-K merge
+    tasks that stopped waiting) and ``split_prefill_merges`` (split prefill
+    item pairs merged).  Raises like ``check_workspaces`` when a merge gave up.
+    Synchronises; a diagnostic for tests and tuning."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(index)
+    if ws is None:
+        return {"merges_gave_up": 0, "split_prefill_merges": 0}
+    ev = (ctypes.c_uint32 * 4)()
+    _lib.check(_lib.load().slo_attention_workspace_check(ws.data_ptr(), ws.numel(), ev, _stream(device)),
+               "slo_attention_workspace_check")
+    return {"merges_gave_up": int(ev[0]), "split_prefill_merges": int(ev[1])}
+
+
 def reserve_workspace(device, max_decode_rows: int, max_decode_len: int, num_heads: int,
                       num_kv_heads: int, head_dim: int) -> torch.Tensor:
     nbytes = _lib.workspace_bytes(max_decode_rows, max_decode_len, num_heads, num_kv_heads, head_dim)

@@ -20,3 +20,17 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _workspace_zero_after_gpu_test(request):
+    """After every GPU test: each attention workspace's work-list counters and
+    split-K tickets are back at zero (the launch contract of include/slo_attn.h)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import torch
+    if not torch.cuda.is_available():
+        return
+    from slo_attn import check_workspaces
+    check_workspaces()

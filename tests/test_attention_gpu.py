@@ -153,11 +153,17 @@ def test_prefill_rows_split_in_key_halves(device, kv_fp8, phases):
     # long-prefix rows split beside unsplit lighter and cold rows (odd tile
     # counts: 4096 + 512 keys end mid-tile for the 16-position blocks).
     # Second: one row of 1,100 new tokens after 1,100 cached ones, alone.
+    from slo_attn import workspace_events
     cases = (Case([], [4096, 0, 2900, 1, 130], [512, 700, 96, 33, 5], seed=12, kv_fp8=kv_fp8),
              Case([], [1100], [1100], seed=13, kv_fp8=kv_fp8))
     for case in cases:
+        workspace_events(device)
         (mx, mn), got, _ = _check(case, device, phases)
-        print(f"split prefill fp8={kv_fp8} phases={phases}: max-abs {mx:.3e} mean-abs {mn:.3e}")
+        merged = workspace_events(device)["split_prefill_merges"]
+        print(f"split prefill fp8={kv_fp8} phases={phases}: max-abs {mx:.3e} mean-abs {mn:.3e}, "
+              f"split pairs merged {merged}")
+        # no decode rows: both phase masks make prefill-only launches, which split
+        assert merged > 0, "no prefill item was split"
         # the merge's rounding does not depend on which half finishes second
         for _ in range(3):
             again, _ = case.run_gpu(device, phases)
@@ -182,3 +188,32 @@ def test_deterministic_across_launches(device):
     b, _ = case.run_gpu(device)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("index,kv_fp8", [(0, False), (3, False), (3, True), (4, False)])
+def test_merge_that_gives_up_is_reported_and_does_not_poison_the_next_launch(device, monkeypatch, index, kv_fp8):
+    # A split-K merge task waits a bounded time for the chunks of its (row, kv
+    # head).  With the bound set to 0 from the host (SLO_ATTN_MERGE_WAIT_US),
+    # tasks whose chunks are not all in give up at once: every kernel still
+    # exits, the host's check raises, the tickets are back at zero, and the
+    # next launch with the normal bound is bit-identical to an untouched one.
+    from slo_attn import check_workspaces, workspace_events
+    case = _workload_case(index, kv_fp8)
+    clean, _ = case.run_gpu(device)
+    check_workspaces()
+    monkeypatch.setenv("SLO_ATTN_MERGE_WAIT_US", "0")
+    gave_up = 0
+    for _ in range(3):
+        case.run_gpu(device)
+        torch.cuda.synchronize()
+        try:
+            gave_up += workspace_events(device)["merges_gave_up"]
+        except RuntimeError as e:
+            assert "gave up waiting" in str(e), e
+            gave_up += int(str(e).split("workspace_check: ")[1].split()[0])
+    print(f"config {index} fp8={kv_fp8}: merges that gave up over 3 launches: {gave_up}")
+    assert gave_up > 0, "no merge task gave up: the bounded wait's exit did not run"
+    monkeypatch.delenv("SLO_ATTN_MERGE_WAIT_US")
+    again, _ = case.run_gpu(device)
+    check_workspaces()
+    assert torch.equal(clean.view(torch.int16), again.view(torch.int16))

@@ -41,7 +41,7 @@ def test_workspace_bytes_and_errors():
     # one record of G x (128 accumulators + m + l + 2 pad) floats per chunk of at least 128 tokens
     per_item = 4 * (128 + 4) * 4
     assert n2 - n1 == 24 * (4096 // 128) * 8 * per_item
-    # control words, 65536 tickets and 48 MiB of split prefill records
+    # control lines, trash and event line, 65536 tickets and 48 MiB of split prefill records
     assert n0 == 24 * 128 + 1024 + 4 * 65536 + (48 << 20)
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.workspace_bytes(1, 1, 32, 8, 64)
@@ -68,6 +68,10 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     args.workspace = 8192
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
     assert "block_size" in lib.slo_last_error().decode()
+    # the workspace check refuses a missing or too small workspace before any HIP call
+    assert lib.slo_attention_workspace_check(None, 1 << 20, None, None) == 1
+    assert lib.slo_attention_workspace_check(8192, 1024, None, None) == 1
+    assert "control area" in lib.slo_last_error().decode()
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 0, 8, 128, 0, None, None, None, None, 0, 1.0, None) == 0
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 4, 8, 96, 0, None, None, None, None, 0, 1.0, None) == 4
     assert lib.slo_store_kvcache(None, 0, None, 0, None, 4, 8, 128, 0, None, None, None, None, 0, 1.0, None) == 1
