@@ -255,12 +255,34 @@ int slo_paged_attention(const slo_paged_attention_args* args, slo_stream_t strea
  * gave up since the last check (their decode outputs are invalid).  When
  * `events` is not NULL it receives the 4 event counters, [0] merges that gave
  * up, [1] split prefill item pairs merged, [2..3] zero; the counters are
- * cleared, so each event is reported once.  It synchronises, so it refuses a
- * stream under capture.  No counterpart in the reference (flash-attn keeps no
+ * cleared, so each event is reported once.  With workspace NULL and
+ * workspace_bytes 0 it checks the static scratch of slo_paged_attention_noalloc
+ * on the current device.  It synchronises, so it refuses a stream under
+ * capture.  No counterpart in the reference (flash-attn keeps no
  * state between calls): it backs the contract of slo_paged_attention.
  */
 int slo_attention_workspace_check(const void* workspace, size_t workspace_bytes, uint32_t* events,
                                   slo_stream_t stream);
+
+/*
+ * slo_paged_attention without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (its
+ * flash-attn calls allocate their own outputs).  Same arguments and results as
+ * slo_paged_attention except that args->workspace must be NULL and
+ * args->workspace_bytes 0: the launch uses the library's static device array
+ * of SLO_NOALLOC_SCRATCH_BYTES per GPU (zero at load, held until the process
+ * ends; its address is looked up once per device), and calls nothing that
+ * allocates.  A launch whose decode rows need more split-K partials than the
+ * array holds after its 260 KiB control area (rows x ceil(table width x
+ * block_size / 128) x num_heads x 528 bytes) is refused with
+ * SLO_ERR_UNSUPPORTED.  Every call on one GPU shares its array, so calls that
+ * overlap on one GPU (several streams, several threads) race; order them on
+ * one stream.  slo_attention_workspace_check(NULL, 0, ...) checks this array
+ * on the current device.
+ */
+#define SLO_NOALLOC_SCRATCH_BYTES (64u << 20)
+int slo_paged_attention_noalloc(const slo_paged_attention_args* args, slo_stream_t stream);
 
 /* Description of the last error on the calling thread ("" if none). */
 const char* slo_last_error(void);

@@ -168,6 +168,9 @@ struct Params {
   // How long a split-K merge task waits for its chunks before it gives up
   // (s_memrealtime ticks).
   int64_t merge_wait_ticks;
+  // Bytes at the start of the partials area that split prefill items may use
+  // for their records (prefill-only launches, which have no decode partials).
+  int64_t pf_split_bytes;
 };
 
 // The two tile stages live in two separate __shared__ arrays of STAGE_BYTES
@@ -1629,7 +1632,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // than twice a workgroup's share of the work (and at least 16), after a
   // cached prefix at least as long as its chunk, is split in
   // two key ranges per item, merged by the range that finishes second, when
-  // every item of the launch has a record slot (a ticket and PF_SPLIT_BYTES
+  // every item of the launch has a record slot (a ticket and pf_split_bytes
   // of records); such a row otherwise sets the launch's length alone.
   if constexpr (MODE == MODE_PREFILL) {
     int base_c = 0, extra_c = 0;
@@ -1653,7 +1656,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     if (tid == 0) {
       const int all = sm.wsum[0] + sm.wsum[1] + sm.wsum[2] + sm.wsum[3];
       const int ext = sm.dsum[0] + sm.dsum[1] + sm.dsum[2] + sm.dsum[3];
-      const int cap = (int)(PF_SPLIT_BYTES / (sizeof(float) * (size_t)PF_REC_FLOATS * (bq / 16)));
+      const int cap = (int)(p.pf_split_bytes / (int64_t)(sizeof(float) * (size_t)PF_REC_FLOATS * (bq / 16)));
       if (ext == 0 || all + ext > cap || all + ext > MAX_COUNTERS) sm.pf_split_thr = 1 << 30;
     }
     __syncthreads();
@@ -1899,7 +1902,14 @@ extern "C" int slo_attention_workspace_bytes(int32_t max_decode_rows, int32_t ma
   return SLO_OK;
 }
 
-extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream_t stream) {
+namespace slo {
+
+// One launch with workspace `ws` of `ws_bytes` bytes.  `sized` is true for a
+// caller-sized workspace (slo_paged_attention: at least
+// slo_attention_workspace_bytes), false for the library's static scratch,
+// which must hold this launch's decode partials, or split prefill records of
+// up to PF_SPLIT_BYTES, after the control area.
+int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_bytes, bool sized, slo_stream_t stream) {
   if (!a) return fail(SLO_ERR_INVALID, "paged_attention: null args");
   if (a->head_dim != HD) return fail(SLO_ERR_UNSUPPORTED, "paged_attention: head_dim must be 128");
   if (a->num_kv_heads <= 0 || a->num_heads <= 0 || a->num_heads % a->num_kv_heads)
@@ -1913,7 +1923,7 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   if ((do_dec ? a->num_decode : 0) + (do_pf ? a->num_prefill : 0) > MAX_ROWS)
     return fail(SLO_ERR_UNSUPPORTED, "paged_attention: more than 1024 rows in one launch");
   if (!do_dec && !do_pf) return SLO_OK;
-  if (!a->q || !a->out || !a->workspace) return fail(SLO_ERR_INVALID, "paged_attention: null q/out/workspace");
+  if (!a->q || !a->out || !ws) return fail(SLO_ERR_INVALID, "paged_attention: null q/out/workspace");
   if ((a->q_row_stride % 8) || (a->out_row_stride % 8) || (reinterpret_cast<uintptr_t>(a->q) % 16) ||
       (reinterpret_cast<uintptr_t>(a->out) % 16))
     return fail(SLO_ERR_INVALID, "paged_attention: q/out rows must be 16-byte aligned");
@@ -1957,16 +1967,35 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
       return fail(SLO_ERR_INVALID,
                   "paged_attention: new K/V must be contiguous 16-byte aligned bf16 rows, one per query row");
   }
-  // Workspace: control words, split-K tickets, then decode partials.
-  size_t need = 0;
+  // Workspace: control words, split-K tickets, then decode partials (or, in
+  // prefill-only launches, split prefill records).
   const int dec_len_cap = do_dec ? a->decode_table_width * a->block_size : 0;
-  int rc = slo_attention_workspace_bytes(do_dec ? a->num_decode : 0, dec_len_cap, a->num_heads, a->num_kv_heads, HD, &need);
-  if (rc) return rc;
-  if (a->workspace_bytes < need) return fail(SLO_ERR_WORKSPACE, "paged_attention: workspace too small");
-  if (reinterpret_cast<uintptr_t>(a->workspace) % 256) return fail(SLO_ERR_INVALID, "paged_attention: workspace must be 256-byte aligned");
+  int64_t pf_split_bytes = PF_SPLIT_BYTES;
+  if (sized) {
+    size_t need = 0;
+    int rc = slo_attention_workspace_bytes(do_dec ? a->num_decode : 0, dec_len_cap, a->num_heads, a->num_kv_heads, HD,
+                                           &need);
+    if (rc) return rc;
+    if (ws_bytes < need) return fail(SLO_ERR_WORKSPACE, "paged_attention: workspace too small");
+  } else {
+    const int64_t chunks = (dec_len_cap + CHUNK_MIN - 1) / CHUNK_MIN;
+    const size_t dec_bytes =
+        do_dec ? sizeof(float) * partial_floats((int64_t)a->num_decode * std::max<int64_t>(1, chunks) * a->num_kv_heads, G)
+               : 0;
+    if (ws_bytes < PARTIALS_OFFSET || dec_bytes > ws_bytes - PARTIALS_OFFSET) {
+      char msg[200];
+      snprintf(msg, sizeof msg,
+               "paged_attention_noalloc: %d decode rows of up to %d tokens need %zu bytes of split-K partials; the "
+               "static scratch holds %zu",
+               a->num_decode, dec_len_cap, dec_bytes, ws_bytes - PARTIALS_OFFSET);
+      return fail(SLO_ERR_UNSUPPORTED, msg);
+    }
+    pf_split_bytes = std::min<int64_t>(PF_SPLIT_BYTES, (int64_t)(ws_bytes - PARTIALS_OFFSET));
+  }
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(SLO_ERR_INVALID, "paged_attention: workspace must be 256-byte aligned");
 
   DeviceShape ds;
-  rc = device_shape(&ds);
+  const int rc = device_shape(&ds);
   if (rc) return rc;
 
   Params p{};
@@ -2002,10 +2031,11 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   p.G = G;
   p.HG = (G + 3) / 4;
   p.scale_log2 = a->softmax_scale * kLog2e;
-  char* ws = static_cast<char*>(a->workspace);
-  p.ctrl = reinterpret_cast<int*>(ws);
-  p.counters = reinterpret_cast<int*>(ws + CTRL_BYTES);
-  p.partials = reinterpret_cast<float*>(ws + PARTIALS_OFFSET);
+  char* wsb = static_cast<char*>(ws);
+  p.ctrl = reinterpret_cast<int*>(wsb);
+  p.counters = reinterpret_cast<int*>(wsb + CTRL_BYTES);
+  p.partials = reinterpret_cast<float*>(wsb + PARTIALS_OFFSET);
+  p.pf_split_bytes = pf_split_bytes;
   p.sslots = store ? a->store_slot_mapping : nullptr;
   p.nk = static_cast<const uint16_t*>(a->new_k);
   p.nv = static_cast<const uint16_t*>(a->new_v);
@@ -2045,8 +2075,59 @@ extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream
   return check_launch("paged_attention");
 }
 
+// The allocation-free entry's workspace: one array per GPU, zero when the
+// code object is loaded, its control words and tickets zero again after every
+// launch.  In host code `scratch` is only a stand-in for the device symbol:
+// kernels get the address hipGetSymbolAddress returns for the current device.
+constexpr size_t SCRATCH_BYTES = 64u << 20;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(SLO_ERR_HIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return fail(SLO_ERR_HIP, "paged_attention_noalloc: hipGetSymbolAddress of the static scratch failed");
+    addr[dev] = ptr;
+  }
+  *out = addr[dev];
+  return SLO_OK;
+}
+
+}  // namespace slo
+
+extern "C" int slo_paged_attention(const slo_paged_attention_args* a, slo_stream_t stream) {
+  if (!a) return fail(SLO_ERR_INVALID, "paged_attention: null args");
+  return launch_attention(a, a->workspace, a->workspace_bytes, true, stream);
+}
+
+extern "C" int slo_paged_attention_noalloc(const slo_paged_attention_args* a, slo_stream_t stream) {
+  if (!a) return fail(SLO_ERR_INVALID, "paged_attention_noalloc: null args");
+  if (a->workspace || a->workspace_bytes)
+    return fail(SLO_ERR_INVALID, "paged_attention_noalloc: workspace must be NULL (the static scratch is used)");
+  const bool any = ((a->phases & SLO_PHASE_DECODE) && a->num_decode > 0) ||
+                   ((a->phases & SLO_PHASE_PREFILL) && a->num_prefill > 0);
+  void* ws = nullptr;
+  if (any) {
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+  }
+  return launch_attention(a, ws, SCRATCH_BYTES, false, stream);
+}
+
 extern "C" int slo_attention_workspace_check(const void* workspace, size_t workspace_bytes, uint32_t* events,
                                              slo_stream_t stream) {
+  if (!workspace && !workspace_bytes) {  // the static scratch of slo_paged_attention_noalloc on this device
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+    workspace = ws;
+    workspace_bytes = SCRATCH_BYTES;
+  }
   if (!workspace || workspace_bytes < PARTIALS_OFFSET)
     return fail(SLO_ERR_INVALID, "workspace_check: workspace missing or smaller than its control area");
   hipStream_t s = static_cast<hipStream_t>(stream);

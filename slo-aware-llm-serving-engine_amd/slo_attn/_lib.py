@@ -20,6 +20,7 @@ PHASE_DECODE = 1
 PHASE_PREFILL = 2
 PHASE_ALL = 3
 FP8_SCALE_FLOOR = 2.0 ** -64
+NOALLOC_SCRATCH_BYTES = 64 << 20
 FP8_MAX = 448.0
 
 _c_int32 = ctypes.c_int32
@@ -69,6 +70,7 @@ EXPORTS = (
     "slo_build_mixed_metadata",
     "slo_attention_workspace_bytes",
     "slo_paged_attention",
+    "slo_paged_attention_noalloc",
     "slo_attention_workspace_check",
     "slo_last_error",
     "slo_paged_attention_args_size",
@@ -110,6 +112,8 @@ def load() -> ctypes.CDLL:
             _c_int32, _c_int32, _c_int32, _c_int32, _c_int32, ctypes.POINTER(ctypes.c_size_t)]
         lib.slo_paged_attention.restype = ctypes.c_int
         lib.slo_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_void_p]
+        lib.slo_paged_attention_noalloc.restype = ctypes.c_int
+        lib.slo_paged_attention_noalloc.argtypes = [ctypes.POINTER(PagedAttentionArgs), _c_void_p]
         lib.slo_attention_workspace_check.restype = ctypes.c_int
         lib.slo_attention_workspace_check.argtypes = [_c_void_p, ctypes.c_size_t, _c_void_p, _c_void_p]
         lib.slo_last_error.restype = ctypes.c_char_p

@@ -307,7 +307,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
                     k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                     phases: int = _lib.PHASE_ALL, out: torch.Tensor | None = None,
                     store_slot_mapping: torch.Tensor | None = None, new_k: torch.Tensor | None = None,
-                    new_v: torch.Tensor | None = None) -> torch.Tensor:
+                    new_v: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
     """One ragged launch: decode rows ``q[:num_decode]``, then prefill rows.
 
     Decode row b attends to ``decode_lens[b]`` cached tokens through
@@ -322,6 +322,10 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
     tokens) to their slots, the store of forward_mixed folded in, and reads the
     step's new tokens from those rows; the result is the separate store
     followed by the launch, bit for bit.
+
+    ``noalloc=True`` launches through ``slo_paged_attention_noalloc``, which
+    uses the library's static per-GPU scratch instead of this module's
+    workspace (pass ``out`` as well and nothing is allocated).
     """
     if q.dim() != 3:
         raise ValueError("q must be [tokens, num_heads, head_dim]")
@@ -407,6 +411,11 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
     args.num_heads, args.num_kv_heads, args.head_dim = num_heads, num_kv_heads, head_dim
     args.softmax_scale = float(softmax_scale)
     args.phases = int(phases)
+    if noalloc:
+        args.workspace, args.workspace_bytes = None, 0
+        _lib.check(_lib.load().slo_paged_attention_noalloc(ctypes.byref(args), _stream(device)),
+                   "slo_paged_attention_noalloc")
+        return out
     need = _lib.workspace_bytes(num_decode if (phases & _lib.PHASE_DECODE) else 0,
                                 decode_cap_len, num_heads, num_kv_heads, head_dim)
     ws = workspace(device, need)
