@@ -10,9 +10,14 @@ start position, new tokens and block table; plus the token ids), and the
 captured step begins with ``slo_build_mixed_metadata``, which derives
 positions, slots, decode lengths and cu_seqlens on the GPU.  Rows and tokens
 beyond the step's are inert (slot -1, zero-length rows), so one graph serves
-every batch that fits its bucket.  Inside the graph the prefill rows read
-their keys from the pool (``prefill_has_history=True``), which holds exactly
-the bf16 K/V a cold prefill would read from the new rows.
+every batch that fits its bucket.  By default the prefill rows read their keys
+from the pool (``prefill_has_history=True``): a bf16 pool holds exactly the
+K/V a cold prefill would read from the new rows.  An E4M3FN pool holds their
+quantised codes instead, so the reference's rule (the new rows unless some
+prefill row has a cached prefix, mixed_model_runner.py:88 and
+mixed_attention.py:45-54) needs a second captured graph for steps whose
+prefill rows all start at position 0 (``MixedStepGraph(...,
+exact_history=True)``).
 """
 from __future__ import annotations
 
@@ -93,43 +98,60 @@ class MixedStepBuffers:
             _ptr(self.decode_lens) if self.dc else None, _ptr(self.cu_q), _ptr(self.cu_k), _ptr(self.last_token),
             _stream(self.device)), "slo_build_mixed_metadata")
 
-    def set_context(self) -> None:
-        """Publishes the bucket's Context for the attention layers (context.py:21-28)."""
+    def set_context(self, history: bool = True) -> None:
+        """Publishes the bucket's Context for the attention layers (context.py:21-28).
+
+        ``history`` is ``prefill_has_history``: prefill rows read their keys
+        from the pool (True) or from the step's new K/V rows (False, valid when
+        every prefill row starts at position 0)."""
         meta = MixedAttentionContext(
             self.dc, self.tc - self.dc, self.decode_lens[:self.dc] if self.dc else None,
             self.tables[:self.dc] if self.dc else None, self.cu_q, self.cu_k, self.tables[self.dc:],
-            self.tc - self.dc, self.max_model_len, True)
+            self.tc - self.dc, self.max_model_len, history)
         set_context(False, slot_mapping=self.slot_mapping, mixed=meta)
 
 
 class MixedStepGraph:
     """``fn(input_ids, positions)`` (one model forward over the bucket's tokens)
-    captured together with the metadata launch; ``run`` loads a step and replays."""
+    captured together with the metadata launch; ``run`` loads a step and replays.
 
-    def __init__(self, buffers: MixedStepBuffers, fn, warmup: int = 1):
+    With ``exact_history`` (required for E4M3FN pools) a second graph is
+    captured for steps whose prefill rows all start at position 0, which then
+    attend to their new K/V rows as the reference's ``prefill_has_history``
+    rule says; ``run`` picks the graph from the host-known start positions.
+    The two graphs share the bucket's buffers (and cost two graph memory
+    pools)."""
+
+    def __init__(self, buffers: MixedStepBuffers, fn, warmup: int = 1, exact_history: bool = False):
         self.buffers, self.fn = buffers, fn
-        s = torch.cuda.Stream(device=buffers.device)
-        s.wait_stream(torch.cuda.current_stream(buffers.device))
-        with torch.cuda.stream(s):
-            for _ in range(warmup):
-                self._body()
-        torch.cuda.current_stream(buffers.device).wait_stream(s)
-        torch.cuda.synchronize(buffers.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.output = self._body()
-        reset_context()
+        self.graphs, self.outputs = {}, {}
+        for history in ((False, True) if exact_history else (True,)):
+            s = torch.cuda.Stream(device=buffers.device)
+            s.wait_stream(torch.cuda.current_stream(buffers.device))
+            with torch.cuda.stream(s):
+                for _ in range(warmup):
+                    self._body(history)
+            torch.cuda.current_stream(buffers.device).wait_stream(s)
+            torch.cuda.synchronize(buffers.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self.outputs[history] = self._body(history)
+            self.graphs[history] = graph
+            reset_context()
+        self.graph, self.output = self.graphs[True], self.outputs[True]
 
-    def _body(self):
+    def _body(self, history: bool = True):
         b = self.buffers
         b.build()
-        b.set_context()
+        b.set_context(history)
         try:
             return self.fn(b.input_ids, b.positions)
         finally:
             reset_context()
 
     def run(self, decode_start, prefill_rows, tables, input_ids) -> torch.Tensor:
+        """Loads the step and replays its graph; returns the (static) output."""
+        history = any(s > 0 for s, n in prefill_rows if n) if False in self.graphs else True
         self.buffers.load(decode_start, prefill_rows, tables, input_ids)
-        self.graph.replay()
-        return self.output
+        self.graphs[history].replay()
+        return self.outputs[history]

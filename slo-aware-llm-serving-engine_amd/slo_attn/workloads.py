@@ -123,25 +123,30 @@ def build(name: str, seed: int, decode_lens: list[int], prefill_q: list[int],
                     extra={"seed": seed})
 
 
-def config(index: int) -> Workload:
-    """The attention-layer workloads of the five benchmark configurations."""
+def config(index: int, hq: int = HQ, hkv: int = HKV) -> Workload:
+    """The attention-layer workloads of the five benchmark configurations.
+
+    ``hq``/``hkv`` select the heads of one tensor-parallel rank (16 and 4 at
+    TP=2, qwen3.py:29-35); row lengths, block tables and slots are drawn
+    before the values, so they are the same whatever the head counts."""
     g = torch.Generator().manual_seed(index)
+    tag = "" if (hq, hkv) == (HQ, HKV) else f"_{hq}q{hkv}kv"
     if index == 0:
         lens = torch.randint(64, 1025, (16,), generator=g).tolist()
-        return build("decode16_ctx64-1024", 0, lens, [], [], 128, g)
+        return build("decode16_ctx64-1024" + tag, 0, lens, [], [], 128, g, hq, hkv)
     if index == 1:
         lens = torch.randint(256, 2049, (4,), generator=g).tolist()
-        return build("prefill4_varlen256-2048", 1, [], lens, [0] * 4, 64, g)
+        return build("prefill4_varlen256-2048" + tag, 1, [], lens, [0] * 4, 64, g, hq, hkv)
     if index == 2:
         idx = torch.randint(0, 4, (3,), generator=g).tolist()
         prefixes = [(0, 512, 1024, 2048)[i] for i in idx]
-        return build("chunked_prefill3x512_prefix", 2, [], [512] * 3, prefixes, 96, g)
+        return build("chunked_prefill3x512_prefix" + tag, 2, [], [512] * 3, prefixes, 96, g, hq, hkv)
     if index == 3:
         lens = torch.randint(256, 4097, (24,), generator=g).tolist()
-        return build("mixed_24decode_2x512chunk", 3, lens, [512, 512], [0, 1024], 512, g)
+        return build("mixed_24decode_2x512chunk" + tag, 3, lens, [512, 512], [0, 1024], 512, g, hq, hkv)
     if index == 4:
         lens = torch.randint(512, 4097, (64,), generator=g).tolist()
-        return build("qwen3_4b_layer_64decode_1024chunk", 4, lens, [1024], [0], 681, g)
+        return build("qwen3_4b_layer_64decode_1024chunk" + tag, 4, lens, [1024], [0], 681, g, hq, hkv)
     raise ValueError(index)
 
 

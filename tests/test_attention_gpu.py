@@ -93,11 +93,11 @@ def test_corrupt_old_values_are_detected(device):
 
 
 # --------------------------------------------- benchmark configurations
-def _workload_case(index, kv_fp8=False):
+def _workload_case(index, kv_fp8=False, hq=32, hkv=8):
     from slo_attn import workloads
-    w = workloads.config(index)
+    w = workloads.config(index, hq, hkv)
     nd = w.num_decode
-    case = Case([L - 1 for L in w.decode_lens], w.prefill_prefix, w.prefill_q, seed=1000 + index,
+    case = Case([L - 1 for L in w.decode_lens], w.prefill_prefix, w.prefill_q, hq=hq, hkv=hkv, seed=1000 + index,
                 kv_fp8=kv_fp8, tables=w.decode_tables + w.prefill_tables, num_blocks=w.k_cache.shape[0])
     # use the workload's own values so the test runs the benchmarked inputs
     case.q, case.k, case.v = w.q, w.k, w.v
@@ -125,6 +125,15 @@ def test_benchmark_config_fp8(device, index):
     print(f"config {index} fp8: max-abs {mx:.3e} mean-abs {mn:.3e}")
 
 
+@pytest.mark.parametrize("index,kv_fp8", [(3, False), (3, True), (4, False), (4, True)])
+def test_benchmark_config_tp2_rank_shape(device, index, kv_fp8):
+    # one tensor-parallel rank at TP=2: 16 query and 4 kv heads (qwen3.py:29-35,
+    # README.md:9), same rows, tables and slots as the full-head workload
+    case = _workload_case(index, kv_fp8, hq=16, hkv=4)
+    (mx, mn), _, _ = _check(case, device)
+    print(f"config {index} at 16/4 heads fp8={kv_fp8}: max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
 # --------------------------------------------- boundaries and padding
 @pytest.mark.parametrize("kv_fp8", [False, True])
 def test_decode_length_boundaries(device, kv_fp8):
@@ -138,7 +147,7 @@ def test_prefill_tile_and_prefix_boundaries(device):
     _check(Case([5, 300], prefixes, counts, seed=8), device)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (64, 8), (16, 1), (12, 4)])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (64, 8), (16, 1), (12, 4), (16, 4)])
 def test_gqa_ratios(device, hq, hkv):
     _check(Case([100, 700], [40, 0], [70, 33], hq=hq, hkv=hkv, seed=hq * 10 + hkv), device)
 

@@ -10,6 +10,11 @@
   steps; every replay equals the same padded step run eagerly, bit for bit
   (hidden states and pool bytes), and its real tokens agree with an unpadded
   eager run of the step within bf16 GEMM noise (the GEMMs see more rows).
+  With an E4M3FN pool the step graph is captured twice (``exact_history``):
+  a step whose prefill rows all start at position 0 replays the graph in which
+  they attend to their new bf16 K/V, as the eager path and the reference's
+  ``prefill_has_history`` rule do (mixed_model_runner.py:88); the first step of
+  each run is such a step.
 """
 import numpy as np
 import pytest
@@ -23,9 +28,11 @@ from slo_attn import Attention, KVPool, MixedStepBuffers, MixedStepGraph, MixedA
 pytestmark = pytest.mark.gpu
 
 
-def _rand_step(g, dc, pc, tc, width, bs, nblk):
+def _rand_step(g, dc, pc, tc, width, bs, nblk, cold=False):
     d = int(torch.randint(0, dc + 1, (1,), generator=g))
     r = int(torch.randint(0, pc + 1, (1,), generator=g))
+    if cold:  # a step whose prefill rows all start at position 0: at least two of them, with tokens
+        r = max(r, min(pc, 2))
     budget = tc - dc
     perm = torch.randperm(nblk, generator=g).tolist()
     tables, rows, at = [], [], 0
@@ -36,9 +43,9 @@ def _rand_step(g, dc, pc, tc, width, bs, nblk):
         tables.append(perm[at:at + n]); at += n
         dstart.append(s)
     for i in range(r):
-        n = int(torch.randint(0, max(1, budget // max(r, 1)) + 1, (1,), generator=g))
+        n = int(torch.randint(1 if cold else 0, max(1, budget // max(r, 1)) + 1, (1,), generator=g))
         budget -= n
-        s = int(torch.randint(0, width * bs - n - 1, (1,), generator=g)) if n else 0
+        s = int(torch.randint(0, width * bs - n - 1, (1,), generator=g)) if n and not cold else 0
         k = (s + n + bs - 1) // bs if n else 1
         tables.append(perm[at:at + k]); at += k
         rows.append((s, n))
@@ -74,57 +81,74 @@ def test_metadata_kernel_matches_oracle(device, seed):
         assert want["cu_seqlens_q"][:len(rows) + 1] == m["prefill_cu_q"]
 
 
-def test_graph_replays_equal_eager(device):
+@pytest.mark.parametrize("kv", ["bf16", "fp8_e4m3fn"])
+def test_graph_replays_equal_eager(device, kv):
     geom = Geometry(num_layers=2, hidden=256, num_heads=8, num_kv_heads=2, intermediate=512, vocab=1000,
                     max_position=4096)
     model = Qwen3(geom, device, seed=7)
     model.fused = True
     dc, pc, tc, width, bs, nblk = 6, 3, 256, 8, 64, 160
     g = torch.Generator().manual_seed(11)
+    fp8 = kv != "bf16"
 
-    def fresh_pool():
-        pool = KVPool(geom.num_layers, nblk, bs, geom.num_kv_heads, geom.head_dim, "bf16", device)
-        pool.kv.copy_(torch.randn(pool.kv.shape, generator=g).to(torch.bfloat16))
+    def new_pool(src=None):
+        pool = KVPool(geom.num_layers, nblk, bs, geom.num_kv_heads, geom.head_dim, kv, device)
+        if src is not None:
+            copy_pool(pool, src)
         return pool
 
-    base = fresh_pool()
+    def copy_pool(dst, src):
+        dst.kv.copy_(src.kv)
+        if fp8:
+            dst.scale.copy_(src.scale)
+
+    def pools_equal(a, b):
+        bits = torch.uint8 if fp8 else torch.int16
+        return torch.equal(a.kv.view(bits), b.kv.view(bits)) and (
+            not fp8 or torch.equal(a.scale.view(torch.int32), b.scale.view(torch.int32)))
+
+    base = new_pool()
+    x = torch.randn(base.kv.shape, generator=g)
+    if fp8:  # E4M3FN codes of N(0, 1) values with unit scales
+        base.kv.copy_(x.to(torch.float8_e4m3fn).view(torch.uint8))
+    else:
+        base.kv.copy_(x.to(torch.bfloat16))
     mods = [Attention(geom.num_heads, geom.head_dim, model.scale, geom.num_kv_heads) for _ in range(2)]
     model.attn = mods
-    graph_pool = KVPool(geom.num_layers, nblk, bs, geom.num_kv_heads, geom.head_dim, "bf16", device)
-    graph_pool.kv.copy_(base.kv)
+    graph_pool = new_pool(base)
     graph_pool.attach(mods)
     buf = MixedStepBuffers(dc, pc, tc, width, bs, width * bs, device)
     buf.load([5], [(0, 3)], [[0], [1]], [1, 2, 3, 4])  # any step fits for the capture warmup
-    step = MixedStepGraph(buf, lambda ids, pos: model.forward(ids, pos))
-    graph_pool.kv.copy_(base.kv)  # the warmup and capture wrote KV; start the replays from the base pool
+    step = MixedStepGraph(buf, lambda ids, pos: model.forward(ids, pos), exact_history=fp8)
+    copy_pool(graph_pool, base)  # the warmup and capture wrote KV; start the replays from the base pool
 
     eager_buf = MixedStepBuffers(dc, pc, tc, width, bs, width * bs, device)
-    eager_pool = KVPool(geom.num_layers, nblk, bs, geom.num_kv_heads, geom.head_dim, "bf16", device)
-    eager_pool.kv.copy_(base.kv)
+    eager_pool = new_pool(base)
     for trial in range(3):
-        dstart, rows, tables = _rand_step(g, dc, pc, tc, width, bs, nblk)
+        dstart, rows, tables = _rand_step(g, dc, pc, tc, width, bs, nblk, cold=trial == 0)
         d = len(dstart)
         n_tok = d + sum(n for _, n in rows)
+        history = any(s0 > 0 for s0, n in rows if n) or not fp8
         ids = torch.randint(0, geom.vocab, (n_tok,), generator=g).tolist()
         out = step.run(dstart, rows, tables, ids).clone()
         # the same padded step, eagerly, on a pool in the same state
-        before = eager_pool.kv.clone()
+        before = new_pool(eager_pool)
         eager_pool.attach(mods)
         eager_buf.load(dstart, rows, tables, ids)
         eager_buf.build()
-        eager_buf.set_context()
+        eager_buf.set_context(history)
         try:
             want = model.forward(eager_buf.input_ids, eager_buf.positions)
         finally:
             reset_context()
         torch.cuda.synchronize()
+        print(f"{kv} step {trial}: {d} decode rows, prefill rows {rows}, prefill_has_history={history}")
         assert torch.isfinite(out.float()).all(), "padding rows must stay finite"
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {trial} differs from eager"
-        assert torch.equal(graph_pool.kv.view(torch.int16), eager_pool.kv.view(torch.int16))
+        assert pools_equal(graph_pool, eager_pool)
         # the real tokens against the unpadded step (prepare_mixed metadata, eager)
         if n_tok:
-            ref_pool = KVPool(geom.num_layers, nblk, bs, geom.num_kv_heads, geom.head_dim, "bf16", device)
-            ref_pool.kv.copy_(before)
+            ref_pool = new_pool(before)
             ref_pool.attach(mods)
             m = metadata.mixed_metadata([s0 + 1 for s0 in dstart], tables[:d], [s0 for s0, _ in rows],
                                         [n for _, n in rows], tables[d:])
