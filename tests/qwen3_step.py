@@ -43,6 +43,19 @@ from oracle import metadata
 from slo_attn import KVPool, MixedAttentionContext, get_context, qk_norm_rope_store, reset_context, set_context
 
 
+# Residual-branch conditioning of the full config-4 step.  With plain N(0, 0.02)
+# weights every MLP adds about 1.2 RMS to a residual that starts at the
+# embedding's 0.02, so the final hidden state is close to Gaussian noise: the
+# 151936 logits of a row are Gaussian and their top two often share one bf16
+# value, and two exact evaluations (fp32, fp64) pick different tokens.  Scaling
+# o_proj and down_proj down makes each layer add a few percent of the residual,
+# so the embedding keeps most of it: with the tied LM head a row's own token
+# then wins by a wide margin (at least 3.6 logits, against 0.25 between the
+# exact evaluations), while attention still carries the rest of the logit
+# vector (zeroing it changes the logits by 130% in relative L2).
+CONDITIONED = dict(o_proj_std=4e-4, down_proj_std=2.6e-5)
+
+
 @dataclass(frozen=True)
 class Geometry:
     """Qwen3-4B (configs/qwen3_4b.json and its HF config)."""
@@ -57,6 +70,12 @@ class Geometry:
     rope_theta: float = 1e6
     max_position: int = 40960
     init_std: float = 0.02
+    # Residual-branch conditioning of the random init: the std of o_proj and
+    # down_proj (the two projections that write into the residual stream),
+    # and the q/k norm weights (None: init_std and 1, plain N(0, init_std)).
+    o_proj_std: float | None = None
+    down_proj_std: float | None = None
+    qk_norm_weight: float = 1.0
 
 
 # ------------------------------------------------------------------ layers
@@ -106,11 +125,14 @@ class Qwen3:
         g = torch.Generator(device=device).manual_seed(seed)
         std, bf = geom.init_std, torch.bfloat16
 
-        def normal(*shape):
-            return torch.empty(shape, dtype=bf, device=device).normal_(0.0, std, generator=g)
+        def normal(*shape, s=std):
+            return torch.empty(shape, dtype=bf, device=device).normal_(0.0, s, generator=g)
 
-        def ones(n):
-            return torch.ones(n, dtype=bf, device=device)
+        def ones(n, value=1.0):
+            return torch.full((n,), value, dtype=bf, device=device)
+
+        o_std = std if geom.o_proj_std is None else geom.o_proj_std
+        down_std = std if geom.down_proj_std is None else geom.down_proj_std
 
         hq, hkv, d, h = geom.num_heads, geom.num_kv_heads, geom.head_dim, geom.hidden
         self.q_size, self.kv_size = hq * d, hkv * d
@@ -119,10 +141,11 @@ class Qwen3:
         for _ in range(geom.num_layers):
             self.layers.append({
                 "qkv": normal(self.q_size + 2 * self.kv_size, h),
-                "o": normal(h, self.q_size),
+                "o": normal(h, self.q_size, s=o_std),
                 "gate_up": normal(2 * geom.intermediate, h),
-                "down": normal(h, geom.intermediate),
-                "input_norm": ones(h), "post_norm": ones(h), "q_norm": ones(d), "k_norm": ones(d),
+                "down": normal(h, geom.intermediate, s=down_std),
+                "input_norm": ones(h), "post_norm": ones(h),
+                "q_norm": ones(d, geom.qk_norm_weight), "k_norm": ones(d, geom.qk_norm_weight),
             })
         self.final_norm = ones(h)
         self.rope = rope_table(geom, device)

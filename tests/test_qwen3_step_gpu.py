@@ -1,34 +1,30 @@
 """Full Qwen3-4B mixed forward step with the HIP attention path as a drop-in.
 
-Random-init bf16 weights (seed 4, N(0, 0.02), unit norm weights), 36 layers,
-hidden 2560, 32 query / 8 kv heads of 128, SwiGLU 9728, vocab 151936, RoPE
-theta 1e6.  Batch: 64 decode rows with end_pos uniform in [512, 4096] and one
-1024-token prefill chunk without a cached prefix, all in one mixed step over a
-pool of 681 blocks of 256 tokens whose cached prefixes are N(0, 1).  The same
-model runs three times: with ``slo_attn.Attention`` in every layer, with the
-oracle's attention in fp32 (the reference: store, decode and varlen of
-nanovllm/layers/mixed_attention.py:29-57), and with the oracle evaluated in
-fp64 (a control).  For the bf16 pool and for the E4M3FN pool with
-per-(token, kv head) fp32 scales:
+Random-init bf16 weights (seed 4), 36 layers, hidden 2560, 32 query / 8 kv
+heads of 128, SwiGLU 9728, vocab 151936, RoPE theta 1e6, tied LM head, with
+the residual-branch conditioning of ``qwen3_step.CONDITIONED`` (o_proj and
+down_proj scaled down so that every row's greedy token is decided by a clear
+margin; see there).  Batch: 64 decode rows with end_pos uniform in [512, 4096]
+and one 1024-token prefill chunk without a cached prefix, all in one mixed step
+over a pool of 681 blocks of 256 tokens whose cached prefixes are N(0, 1).  The
+same model runs three times: with ``slo_attn.Attention`` in every layer, with
+the oracle's attention in fp32 (the reference: store, decode and varlen of
+nanovllm/layers/mixed_attention.py:29-57), and with the oracle in fp64 (a
+control).  For the bf16 pool, the E4M3FN pool with per-(token, kv head) fp32
+scales, and the E4M3FN pool with the fused q/k norm + RoPE + KV write:
 
-* greedy tokens.  With random weights the 151936 logits of a row are close to
-  Gaussian, so the top two are often within one bf16 ulp of each other (the LM
-  head's output is bf16); any change of rounding anywhere in the 36 layers then
-  picks the other one.  The fp32 and fp64 evaluations of the same exact
-  attention are such a change, so their logit difference is the noise floor
-  ``tau`` of the check.  Every sampled row (the 64 decode rows and the chunk's
-  last token, mixed_model_runner.py:115-126) must pick a token whose
-  reference logit is within ``tau`` of the reference's maximum, which means
-  the same greedy token wherever the reference's top-2 gap exceeds ``tau``,
-  and our logits must stay within 2 tau of the reference's.
+* greedy tokens: every sampled row (the 64 decode rows and the chunk's last
+  token, mixed_model_runner.py:115-126) picks the reference's token (100%), and
+  the fp64 control picks it too; the smallest top-2 margin of the reference and
+  the fp32-vs-fp64 noise floor ``tau`` are printed, and the margin must exceed
+  ``tau``.
+* the reference's acceptance rule on every row's fp32 logits
+  (benchmarks/v1/numerics.py:5-18 as check_v1.py:216-236 applies it): top-1
+  match, relative L2 <= 0.02, cosine >= 0.999, max-abs <= 0.5.
 * every layer's KV write is bit-exact: the bytes at the step's slots are the
   oracle's store of the K/V that layer was given (E4M3FN codes and fp32 scales
   by ``oracle.fp8.quantize_kv``, evaluated over token slices in threads), and
   every other byte of the pool is unchanged.
-
-The third case runs the HIP side with q/k RMSNorm, RoPE and the KV write fused
-into one launch per layer (slo_attn.qk_norm_rope_store, Attention.forward with
-kv_stored=True); the reference side keeps the reference's separate layers.
 """
 from __future__ import annotations
 
@@ -36,7 +32,7 @@ import numpy as np
 import pytest
 import torch
 
-from qwen3_step import (Geometry, Pool, Qwen3, Recorder, ReferenceAttention, config4_batch,
+from qwen3_step import (CONDITIONED, Geometry, Pool, Qwen3, Recorder, ReferenceAttention, config4_batch,
                         quantize_kv, run_step, top2_gaps)
 from slo_attn import Attention
 
@@ -45,7 +41,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def model(device):
-    m = Qwen3(Geometry(), device, seed=4)
+    m = Qwen3(Geometry(**CONDITIONED), device, seed=4)
     yield m
     del m
     torch.cuda.empty_cache()
@@ -84,19 +80,25 @@ def test_qwen3_4b_mixed_step_greedy_and_kv_bytes(device, model, fp8, fused):
 
     tau = (ref_logits - ctl_logits).abs().max().item()
     gaps = top2_gaps(ref_logits)
-    short = ref_logits.amax(dim=-1) - ref_logits.gather(1, tokens[:, None])[:, 0]
-    dlog = (logits - ref_logits).abs().amax(dim=-1)
     rows = tokens.numel()
-    print(f"sampled rows {rows}: greedy = reference in {(tokens == ref_tokens).sum().item()}, "
-          f"= control in {(tokens == ctl_tokens).sum().item()}; control = reference in "
-          f"{(ctl_tokens == ref_tokens).sum().item()}; noise floor tau {tau:.4f}; "
-          f"rows with reference top-2 gap > tau {(gaps > tau).sum().item()}; "
-          f"largest reference-logit shortfall of our token {short.max().item():.4f}; "
-          f"logits max |ours - reference| {dlog.max().item():.4f}", flush=True)
-    bad = (short > tau).nonzero().flatten().tolist()
-    assert not bad, (f"rows {bad}: our greedy token's reference logit is {short[bad].tolist()} below the "
-                     f"reference maximum, beyond the noise floor {tau}")
-    assert dlog.max().item() <= 2 * tau, f"logits differ by {dlog.max().item()} (> 2 tau = {2 * tau})"
+    # the reference's acceptance rule, row by row (numerics.py:5-18, check_v1.py:216-236)
+    rel = (logits - ref_logits).norm(dim=-1) / ref_logits.norm(dim=-1).clamp_min(1e-12)
+    cos = torch.nn.functional.cosine_similarity(logits, ref_logits, dim=-1)
+    max_abs = (logits - ref_logits).abs().amax(dim=-1)
+    top1 = tokens == ref_tokens
+    ok = top1 & (rel <= 0.02) & (cos >= 0.999) & (max_abs <= 0.5) & torch.isfinite(rel)
+    print(f"sampled rows {rows}: greedy = reference in {int(top1.sum())}/{rows}, control (fp64) = reference in "
+          f"{int((ctl_tokens == ref_tokens).sum())}/{rows}; smallest reference top-2 margin {gaps.min().item():.3f}, "
+          f"noise floor tau {tau:.4f}; reference policy passed by {int(ok.sum())}/{rows} rows "
+          f"(worst rel-L2 {rel.max().item():.4f}, cosine {cos.min().item():.6f}, max-abs {max_abs.max().item():.4f})",
+          flush=True)
+    assert torch.equal(ctl_tokens, ref_tokens), "the fp64 control disagrees with the fp32 reference (conditioning)"
+    assert gaps.min().item() > tau, f"top-2 margin {gaps.min().item()} within the noise floor {tau}"
+    bad = (~top1).nonzero().flatten().tolist()
+    assert not bad, f"rows {bad}: greedy tokens {tokens[bad].tolist()} differ from the reference's {ref_tokens[bad].tolist()}"
+    bad = (~ok).nonzero().flatten().tolist()
+    assert not bad, (f"rows {bad} fail the reference's numerics policy: rel-L2 {rel[bad].tolist()}, cosine "
+                     f"{cos[bad].tolist()}, max-abs {max_abs[bad].tolist()}")
 
     slots = torch.tensor(batch.slots, dtype=torch.long, device=device)
     n = slots.numel()
