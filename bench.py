@@ -11,10 +11,12 @@ kernel and then one attention launch.
 
 Every time below comes from HIP-graph replays: a graph holds back-to-back
 launches that rotate over 4 copies of the pool (4 x 512 MiB bf16), so no
-launch finds its KV in the 256 MB Infinity Cache, and the replays are timed
-with the host clock after an untimed settling phase (~0.3 s of the same
-replays, so the timed ones run at the clocks a serving loop sees).  The
-per-launch time is replay time / launches, gaps between kernels included.
+launch finds its KV in the 256 MB Infinity Cache, after an untimed settling
+phase (~0.3 s of the same replays, so the timed ones run at the clocks a
+serving loop sees).  Per-launch times are HIP events on the replay stream
+around the timed replays / launches, the ~1 us gap between back-to-back
+kernels included; the whole-step throughput uses the host clock between two
+device synchronisations.
 
 * value: whole-step throughput in tokens/s (1048 tokens per step) over the
   --steps timed steps; ms_per_step is the same measurement.
@@ -25,7 +27,7 @@ per-launch time is replay time / launches, gaps between kernels included.
   split launches (decode rows only against HBM, prefill rows only against bf16
   MFMA peak), the mode that mirrors the reference's per-phase flash-attn calls;
   roofline_prefill carries the MFMA-busy fraction that rocprofv3 counters gave
-  for that launch (profiles/counters_*.json).
+  for that launch (profiles/counters_paged_attention.json).
 * roofline_fp8: the same step and split launches on an E4M3FN pool (codes +
   per-(token, kv head) fp32 scales).
 * tp2_rank: the step at one TP=2 rank's head shape (16 query / 4 kv heads, the
@@ -152,7 +154,8 @@ class Step:
 
 def graph_time(fn, n_per_graph=NSETS, target=LAUNCH_TARGET, replays=None):
     """Average time per launch (us) of fn(i), i = 0..n_per_graph-1 captured back to back
-    in one HIP graph, over timed replays after an untimed settling phase."""
+    in one HIP graph: HIP events on the replay stream bracket the timed replays,
+    which follow an untimed settling phase."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -171,13 +174,16 @@ def graph_time(fn, n_per_graph=NSETS, target=LAUNCH_TARGET, replays=None):
             graph.replay()
         torch.cuda.synchronize()
     n = replays if replays is not None else max(1, target // n_per_graph)
-    t0 = time.perf_counter()
+    stream = torch.cuda.current_stream()  # the replays' (and so the kernels') stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
     for _ in range(n):
         graph.replay()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    e1.record(stream)
+    e1.synchronize()
+    dt_ms = e0.elapsed_time(e1)
     del graph
-    return dt * 1e6 / (n * n_per_graph), n * n_per_graph
+    return dt_ms * 1e3 / (n * n_per_graph), n * n_per_graph
 
 
 def hbm(bytes_, us, **extra):
@@ -316,7 +322,7 @@ def main():
     torch.cuda.empty_cache()
 
     traffic = load_profile_json("traffic_mixed_24decode_2x512chunk.json")
-    counters = load_profile_json("counters_prefill_mixed_24decode_2x512chunk.json")
+    counters = load_profile_json("counters_paged_attention.json").get("prefill_3", {})
 
     def traffic_of(kernel):
         return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic else None
