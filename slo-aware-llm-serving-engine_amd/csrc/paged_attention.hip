@@ -185,7 +185,8 @@ struct Smem {
     struct {
       float m[4][4];  // per wavefront, 4 query heads per pass
       float l[4][4];
-    } dec;            // decode: cross-wavefront merge statistics
+      float sc[2][4][64];  // E4M3FN: K (0-31) and V (32-63) scales of a wavefront step, by stage
+    } dec;                 // decode: cross-wavefront merge statistics
     struct {
       float ks[2][TT];
       float vs[2][TT];
@@ -204,7 +205,7 @@ struct Smem {
   int drot;         // decode items rotate kv heads across chunks (long decode launches)
   int pf_split_thr; // prefill-only launches: rows with a heavier block split their keys in two
   int pf_ticket;    // prefill split item: ticket value before this item's arrival
-  int meta[2][8];   // decode: landed row length and block-table entries, by item parity
+  int meta[2][20];  // decode: landed row length and block-table entries, by item parity
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
 
@@ -398,8 +399,9 @@ __device__ __forceinline__ float load_partial(const float* p) {
 // ---------------------------------------------------------------- decode item
 // A decode item (row b, kv head h, chunk c of CHUNK tokens) is NSTEP = 4
 // workgroup steps of DSTEP tokens; in step s wavefront w takes the DT tokens
-// starting at c*CHUNK + s*DSTEP + w*DT.  A workgroup step lies in one KV block
-// (block_size is a multiple of 64).  Step s uses LDS stage s & 1, private to
+// starting at c*CHUNK + s*DSTEP + w*DT (E4M3FN pools: twice as many tokens per
+// wavefront, step and item, d_dt and d_chunk).  A wavefront step lies in one
+// KV block (block_size is a multiple of 64).  Step s uses LDS stage s & 1, private to
 // each wavefront, and the item's Q goes to one half of a double-buffered LDS
 // array, so K, V and Q all go HBM -> LDS through global_load_lds_dwordx4 and
 // no streamed data is held in registers across iterations.  Two steps are in
@@ -433,8 +435,21 @@ constexpr int QBUF = MAX_G * HD * 2;   // bytes of one half of the Q buffer
 static_assert(NSTEP == 4, "the decode loop is written for four workgroup steps per item");
 static_assert(4 * WSTAGE <= STAGE_BYTES, "decode stage must fit the tile stage");
 
+// E4M3FN pools take 32 tokens per wavefront step (two 16-token halves, the
+// same bytes as 16 bf16 tokens), so a wavefront keeps as many bytes in flight
+// as with bf16 and an item of four steps spans 512 tokens.
 template <bool FP8>
-__device__ __forceinline__ constexpr int d_group() { return FP8 ? 5 : 8; }
+__device__ __forceinline__ constexpr int d_dt() { return FP8 ? 2 * DT : DT; }  // tokens per wavefront step
+template <bool FP8>
+__device__ __forceinline__ constexpr int d_step() { return 4 * d_dt<FP8>(); }  // tokens per workgroup step
+template <bool FP8>
+__device__ __forceinline__ constexpr int d_chunk() { return NSTEP * d_step<FP8>(); }  // tokens per item
+template <bool FP8>
+__device__ __forceinline__ constexpr int d_chunk_min() { return d_chunk<FP8>() / 2; }  // two live steps
+// Vector memory operations per wavefront step: bf16 4 K + 4 V; E4M3FN 4 K
+// codes + 4 V codes + 1 of scales.
+template <bool FP8>
+__device__ __forceinline__ constexpr int d_group() { return FP8 ? 9 : 8; }
 
 // s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -531,23 +546,30 @@ __device__ __forceinline__ DMeta decode_geom(const Params& p, int r, int local, 
   return m;
 }
 // Wavefront 0: one LDS DMA of the item's row length (lane 0) and the
-// block-table entries of its steps (lanes 1..NSTEP) into sm.meta[slot].  It
+// block-table entries of its steps (bf16: lanes 1..NSTEP, one per workgroup
+// step; E4M3FN: lanes 1..4*NSTEP, one per step and wavefront, since a
+// 128-token workgroup step may span two blocks of 64) into sm.meta[slot].  It
 // is counted by vmcnt like the KV loads.  (Scalar loads would share lgkmcnt
 // with LDS, so the next LDS wait would stall on their latency; a load into a
 // VGPR could be copied by the compiler before it lands.)
+template <bool FP8>
 __device__ __forceinline__ void decode_meta_dma(const Params& p, Smem& sm, const DMeta& m, int slot, int lane) {
-  const int s = lane - 1;
-  const int32_t* src =
-      (s >= 0 && s < NSTEP)
-          ? p.dtab + (int64_t)m.b * p.dtab_stride + min((m.tok0 + s * DSTEP) / p.block_size, p.dtab_width - 1)
-          : p.dlens + m.b;
-  if (lane <= NSTEP) dma4(src, lds_addr(sm.meta[slot]));
+  constexpr int NE = FP8 ? 4 * NSTEP : NSTEP;  // table entries
+  const int e = lane - 1;
+  const int tok = FP8 ? m.tok0 + (e >> 2) * d_step<FP8>() + (e & 3) * d_dt<FP8>() : m.tok0 + e * DSTEP;
+  const int32_t* src = (e >= 0 && e < NE)
+                           ? p.dtab + (int64_t)m.b * p.dtab_stride + min(tok / p.block_size, p.dtab_width - 1)
+                           : p.dlens + m.b;
+  if (lane <= NE) dma4(src, lds_addr(sm.meta[slot]));
 }
-// After a wait that covers the DMA and a barrier.
-__device__ __forceinline__ void decode_meta_read(DMeta& m, const Smem& sm, int slot) {
+// After a wait that covers the DMA and a barrier.  page[s] is the block of
+// this wavefront's tokens of step s.
+template <bool FP8>
+__device__ __forceinline__ void decode_meta_read(DMeta& m, const Smem& sm, int slot, int wave) {
   m.len = __builtin_amdgcn_readfirstlane(sm.meta[slot][0]);
 #pragma unroll
-  for (int s = 0; s < NSTEP; ++s) m.page[s] = __builtin_amdgcn_readfirstlane(sm.meta[slot][1 + s]);
+  for (int s = 0; s < NSTEP; ++s)
+    m.page[s] = __builtin_amdgcn_readfirstlane(sm.meta[slot][1 + (FP8 ? 4 * s + wave : s)]);
 }
 
 // Row of item `item` among rows [lo, nrows), searched by one wavefront.
@@ -563,10 +585,11 @@ __device__ __forceinline__ int find_row(const Smem& sm, int item, int lo, int nr
 
 // Valid tokens of wavefront `wave` in step s of the item (0 for padding
 // blocks and for steps past the item's span).
+template <bool FP8>
 __device__ __forceinline__ int decode_ntok(const Params& p, const DMeta& m, int s, int wave) {
   const int page = m.page[s];
-  if (page < 0 || page >= p.num_blocks || s * DSTEP >= m.span) return 0;
-  return min(max(decode_L(p, m) - (m.tok0 + s * DSTEP + wave * DT), 0), DT);
+  if (page < 0 || page >= p.num_blocks || s * d_step<FP8>() >= m.span) return 0;
+  return min(max(decode_L(p, m) - (m.tok0 + s * d_step<FP8>() + wave * d_dt<FP8>()), 0), d_dt<FP8>());
 }
 
 // The item's G query heads (G*HD bf16, contiguous in the row) to qbuf; each
@@ -580,15 +603,14 @@ __device__ __forceinline__ void decode_issue_q(const Params& p, uint8_t* qbuf, c
 
 // K and V of one wavefront step to the wavefront's stage region `stg`.
 // bf16: K row r at r*ROWB with 16-byte chunk c in slot c ^ (r & 15), V rows
-// from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN: K codes (128 B
-// rows, chunk c in slot c ^ (r & 7)) at 0, V codes likewise at 2048, K scales
-// at 4096 and V scales at 4160.
+// from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN (32 tokens):
+// see below; the scales go to `scl`.
 template <bool FP8, bool FOLD>
-__device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, const DMeta& m, int s, int wave,
-                                             int lane) {
+__device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, float* scl, const DMeta& m, int s,
+                                             int wave, int lane) {
   const int n = lane & 15, g = lane >> 4;
-  const int ntok = decode_ntok(p, m, s, wave);
-  const int t0 = m.tok0 + s * DSTEP + wave * DT;
+  const int ntok = decode_ntok<FP8>(p, m, s, wave);
+  const int t0 = m.tok0 + s * d_step<FP8>() + wave * d_dt<FP8>();
   if (ntok == 0) {
     // A step without valid tokens issues the same number of operations, each
     // a 4-byte load on one lane: counted like the others, nearly free.
@@ -622,23 +644,24 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
       dma16((r == tnew ? vn : vc + r * row) + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
     }
   } else {
+    // 32 tokens: rows 16h..16h+15 go to half h at 4096h (K codes, 128-byte
+    // rows with 16-byte chunk c in slot c ^ (r & 7), then V codes at +2048);
+    // the K and V scales to scl[0..31] and scl[32..63].
     const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
     const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + base;
     const uint32_t dst = lds_addr(stg);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + i * 1024);
+      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + (i >> 1) * 4096 + (i & 1) * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int r = 8 * i + (lane >> 3);
-      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + 2048 + i * 1024);
+      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + (i >> 1) * 4096 + 2048 + (i & 1) * 1024);
     }
-    // Lanes 0-15: K scales of the 16 tokens, lanes 16-31: V scales (lanes
-    // 32-63 repeat them into unused bytes).
-    const float* sc = (lane & 16) ? p.v_scale : p.k_scale;
-    dma4(sc + (slot0 + (lane & 15)) * p.hkv + m.h, dst + 4096);
+    const float* sc = (lane & 32) ? p.v_scale : p.k_scale;
+    dma4(sc + (slot0 + (lane & 31)) * p.hkv + m.h, lds_addr(scl));
   }
 }
 
@@ -646,8 +669,8 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, cons
 // (o, m, l); lane (n, g) holds O^T[d = 16dt + 4g + i][head n] and the
 // statistics of head n.  Scores are in the log2 domain.
 template <bool FP8>
-__device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int ntok, const u32x4 (&qv)[4],
-                                            f32x4 (&o)[8], float& m, float& l, int lane) {
+__device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const float* ksp, const float* vsp, int ntok,
+                                            const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l, int lane) {
   const int n = lane & 15, g = lane >> 4;
   uint8_t* vt = FP8 ? stg : stg + DT * ROWB;  // bf16 V tile (E4M3FN: decoded over the code bytes)
 
@@ -701,8 +724,8 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
 
   f32x4 ksc = f32x4{1, 1, 1, 1}, vsc = f32x4{1, 1, 1, 1};
   if constexpr (FP8) {
-    ksc = __builtin_bit_cast(f32x4, ld16(stg + 4096 + 16 * g));
-    vsc = __builtin_bit_cast(f32x4, ld16(stg + 4160 + 16 * g));
+    ksc = __builtin_bit_cast(f32x4, ld16(ksp + 4 * g));
+    vsc = __builtin_bit_cast(f32x4, ld16(vsp + 4 * g));
   }
   float x[4];
   float mx = NEG_INF;
@@ -754,6 +777,19 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, int n
   for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt], 0, 0, 0);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pl, o[dt], 0, 0, 0);
+}
+
+// One wavefront step: 16 bf16 tokens, or 32 E4M3FN tokens as two halves of 16
+// (the second skipped when it holds no valid token).
+template <bool FP8>
+__device__ __forceinline__ void decode_wstep(const Params& p, uint8_t* stg, const float* scl, int ntok,
+                                             const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l, int lane) {
+  if constexpr (FP8) {
+    decode_step<FP8>(p, stg, scl, scl + 32, min(ntok, DT), qv, o, m, l, lane);
+    if (ntok > DT) decode_step<FP8>(p, stg + 4096, scl + DT, scl + 32 + DT, ntok - DT, qv, o, m, l, lane);
+  } else {
+    decode_step<FP8>(p, stg, nullptr, nullptr, ntok, qv, o, m, l, lane);
+  }
 }
 
 // Cross-wavefront merge.  Per pass of 4 query heads, every wavefront writes
@@ -1006,9 +1042,11 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const bool w0 = wave == 0;
-  const bool half = dchunk < CHUNK;  // steps 2 and 3 of every item are empty
+  const bool half = dchunk < d_chunk<FP8>();  // steps 2 and 3 of every item are empty
   uint8_t* sa = st0 + wave * WSTAGE;  // even steps
   uint8_t* sb = st1 + wave * WSTAGE;  // odd steps
+  float* ca = sm.u.dec.sc[0][wave];   // E4M3FN scales of even and odd steps
+  float* cb = sm.u.dec.sc[1][wave];
   constexpr int GROUP = d_group<FP8>();
   const int hgp = (p.G + 3) >> 2;  // merge stores per wavefront and item
   auto item_of = [&](uint32_t rel) { return decode_base + list + (int)rel * nlist; };
@@ -1018,15 +1056,15 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   const bool rot = sm.drot;
   DMeta cur = decode_geom(p, r0, __builtin_amdgcn_readfirstlane(item_of(rel0) - sm.off[r0]), item_of(rel0), decode_base,
                           dchunk, rot);
-  if (w0) decode_meta_dma(p, sm, cur, 0, lane);
+  if (w0) decode_meta_dma<FP8>(p, sm, cur, 0, lane);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   lds_sync();
-  decode_meta_read(cur, sm, 0);
+  decode_meta_read<FP8>(cur, sm, 0, wave);
   decode_issue_q(p, qbuf, cur, wave, lane);
-  decode_issue<FP8, FOLD>(p, sa, cur, 0, wave, lane);
+  decode_issue<FP8, FOLD>(p, sa, ca, cur, 0, wave, lane);
   for (int i = 0; i < hgp; ++i)
     if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
-  decode_issue<FP8, FOLD>(p, sb, cur, 1, wave, lane);
+  decode_issue<FP8, FOLD>(p, sb, cb, cur, 1, wave, lane);
   uint32_t f = 0;
   bool fetching = true;  // the fetch in flight is a real one
   if (tid == 0) f = atomic_add_ret(ctr, 1u);
@@ -1050,8 +1088,8 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
     float m = NEG_INF, l = 0.0f;
-    decode_step<FP8>(p, sa, decode_ntok(p, cur, 0, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, cur, 2, wave, lane);
+    decode_wstep<FP8>(p, sa, ca, decode_ntok<FP8>(p, cur, 0, wave), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sa, ca, cur, 2, wave, lane);
 
     // Step 1: (cur, 1) has landed, and with it prev's stores (every
     // wavefront's, after the barrier) and the fetch.  Wavefront 0 finds the
@@ -1078,10 +1116,10 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
         }
         if (tid == 0) sm.item = rel1;
       }
-      decode_meta_dma(p, sm, nxt, (k + 1) & 1, lane);
+      decode_meta_dma<FP8>(p, sm, nxt, (k + 1) & 1, lane);
     }
-    decode_step<FP8>(p, sb, decode_ntok(p, cur, 1, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sb, cur, 3, wave, lane);
+    decode_wstep<FP8>(p, sb, cb, decode_ntok<FP8>(p, cur, 1, wave), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sb, cb, cur, 3, wave, lane);
 
     // Step 2: (cur, 2) and nxt's metadata have landed; the broadcast is
     // visible after the barrier.
@@ -1094,20 +1132,20 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
         if (!w0)
           nxt = decode_geom(p, __builtin_amdgcn_readfirstlane(sm.bcast[0]),
                             __builtin_amdgcn_readfirstlane(sm.bcast[1]), item_of(rel1), decode_base, dchunk, rot);
-        decode_meta_read(nxt, sm, (k + 1) & 1);
+        decode_meta_read<FP8>(nxt, sm, (k + 1) & 1, wave);
       }
     }
     if (!has1) nxt = cur;  // no next item: its loads repeat the current item's
     decode_issue_q(p, qnxt, nxt, wave, lane);
-    if (!half) decode_step<FP8>(p, sa, decode_ntok(p, cur, 2, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, nxt, 0, wave, lane);
+    if (!half) decode_wstep<FP8>(p, sa, ca, decode_ntok<FP8>(p, cur, 2, wave), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sa, ca, nxt, 0, wave, lane);
 
     // Step 3: (cur, 3) has landed.
     wait_vm<GROUP + 1>(0);
-    if (!half) decode_step<FP8>(p, sb, decode_ntok(p, cur, 3, wave), qv, o, m, l, lane);
+    if (!half) decode_wstep<FP8>(p, sb, cb, decode_ntok<FP8>(p, cur, 3, wave), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
-    decode_issue<FP8, FOLD>(p, sb, nxt, 1, wave, lane);
+    decode_issue<FP8, FOLD>(p, sb, cb, nxt, 1, wave, lane);
     fetching = fetching && has1;
     if (tid == 0) f = atomic_add_ret(ctr, fetching ? 1u : 0u);
     prev = cur;
@@ -1541,10 +1579,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // tiles loaded per query); a prefill-only launch uses 16 when the heaviest
   // 32-position block would take more than twice a workgroup's fair share of
   // the work (the launch would wait on that one item), else 32.  Decode chunk:
-  // CHUNK tokens when that still gives at least two items per workgroup,
-  // else CHUNK_MIN (short launches need the parallelism more than the longer
-  // items' lower per-token overhead).
-  int bq = 32, dchunk = CHUNK;
+  // d_chunk tokens (bf16 256, E4M3FN 512) when that still gives at least two
+  // items per workgroup, else half of it (bf16 only: short launches need the
+  // parallelism more than the longer items' lower per-token overhead).
+  int bq = 32, dchunk = d_chunk<FP8>();
   // Item counts of this thread's rows under either choice (32-position
   // blocks / CHUNK, 16-position blocks / CHUNK_MIN), so the metadata is read
   // once.
@@ -1568,9 +1606,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
         cnt_b[i] = lq > 0 ? ((lq + 15) / 16) * p.hkv * p.HG : 0;
       } else {
         const int L = decode_len(p, r - p.np);
-        dn += (L + CHUNK - 1) / CHUNK;
-        cnt_a[i] = max(1, (L + CHUNK - 1) / CHUNK) * p.hkv;
-        cnt_b[i] = max(1, (L + CHUNK_MIN - 1) / CHUNK_MIN) * p.hkv;
+        dn += (L + d_chunk<FP8>() - 1) / d_chunk<FP8>();
+        cnt_a[i] = max(1, (L + d_chunk<FP8>() - 1) / d_chunk<FP8>()) * p.hkv;
+        cnt_b[i] = max(1, (L + d_chunk_min<FP8>() - 1) / d_chunk_min<FP8>()) * p.hkv;
       }
     }
 
@@ -1595,7 +1633,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       dt += sm.dsum[i];
     }
     if (MODE == MODE_PREFILL && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
-    if (dt * p.hkv < 2 * (int64_t)gridDim.x) dchunk = CHUNK_MIN;
+    // (E4M3FN launches always take full 512-token items: measured 27.0 ->
+    // 25.5 us on 16 rows of 64-1024 tokens and 54 -> 51 us on 24 rows of
+    // 256-4096, where half items keep half the bytes in flight.)
+    if (!FP8 && dt * p.hkv < 2 * (int64_t)gridDim.x) dchunk = d_chunk_min<FP8>();
     // E4M3FN mixed launches: a prefill row whose heaviest 32-position block
     // spans more key tiles than a workgroup's share of the launch (a decode
     // item counted as 4 tiles) uses 16-position blocks, which halves the
@@ -1667,7 +1708,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   int local_sum = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == CHUNK_MIN;
+    const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == d_chunk_min<FP8>();
     cnt[i] = alt ? cnt_b[i] : cnt_a[i];
     if (MODE == MODE_PREFILL && r0 + i < p.np && pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) cnt[i] *= 2;
     local_sum += cnt[i];

@@ -141,6 +141,17 @@ def test_decode_length_boundaries(device, kv_fp8):
     _check(Case(hist, [], [], seed=7, kv_fp8=kv_fp8), device)
 
 
+@pytest.mark.parametrize("kv_fp8", [False, True])
+def test_decode_small_blocks_and_step_boundaries(device, kv_fp8):
+    # 64-token blocks with pages in random order: an E4M3FN wavefront step is
+    # 32 tokens and a workgroup step 128, so a step's wavefronts read two
+    # blocks; lengths around 16/32-token halves, steps and 256/512-token items.
+    hist = [14, 15, 16, 30, 31, 32, 94, 95, 127, 128, 200, 383, 384, 511, 512, 767, 1100, 2047]
+    _check(Case(hist, [], [], bs=64, seed=17, kv_fp8=kv_fp8), device)
+    # the same rows beside a prefill chunk (mixed launch)
+    _check(Case(hist[:9], [70], [45], bs=64, seed=18, kv_fp8=kv_fp8), device)
+
+
 def test_prefill_tile_and_prefix_boundaries(device):
     counts = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100]
     prefixes = [0, 1, 63, 64, 255, 256, 257, 0, 511, 3, 700]
