@@ -188,8 +188,8 @@ struct Smem {
       float sc[2][4][64];  // E4M3FN: K (0-31) and V (32-63) scales of a wavefront step, by stage
     } dec;                 // decode: cross-wavefront merge statistics
     struct {
-      float ks[2][TT];
-      float vs[2][TT];
+      __attribute__((aligned(16))) float ks[2][TT];
+      __attribute__((aligned(16))) float vs[2][TT];
       int pages[MAX_PAGES];  // block table of the current row
     } pf;                    // prefill
   } u;
@@ -295,9 +295,7 @@ __device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT
   for (int nt = 0; nt < NQT; ++nt) {
     if (src_fp8) {
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sh[mm][nt][i] *= ks[kh + 16 * mm + 4 * g + i];
+      for (int mm = 0; mm < 2; ++mm) sh[mm][nt] *= *reinterpret_cast<const f32x4*>(ks + kh + 16 * mm + 4 * g);
     }
     if constexpr (MASK) {
       const int lim = lim0 + 16 * nt;
@@ -321,13 +319,15 @@ __device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT
     const float a = grow ? __builtin_amdgcn_exp2f(c * m[nt] - cm) : 1.0f;
     float rs = 0.0f;
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm)
+    for (int mm = 0; mm < 2; ++mm) {
+      const f32x4 vsc = src_fp8 ? *reinterpret_cast<const f32x4*>(vs + kh + 16 * mm + 4 * g) : f32x4{1, 1, 1, 1};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float e = __builtin_amdgcn_exp2f(fmaf(sh[mm][nt][i], c, -cm));
         rs += e;
-        sh[mm][nt][i] = src_fp8 ? e * vs[kh + 16 * mm + 4 * g + i] : e;
+        sh[mm][nt][i] = src_fp8 ? e * vsc[i] : e;
       }
+    }
     rs = col_sum(rs);
     l[nt] = l[nt] * a + rs;
     m[nt] = mnew;
@@ -1186,6 +1186,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 
   const int nqb = (Lq + BQ - 1) / BQ;
   const int q0 = (nqb - 1 - qb_rev) * BQ;  // heaviest blocks are pulled first
+  // An item past the row's blocks (its count and block size disagree) reads
+  // and writes nothing.
+  if (q0 < 0) return;
   const int qend = min(q0 + BQ, Lq);
   const int kend = min(Lk, max(0, prefix + qend));
   // Key range of this item: all tiles, or one half (the first half takes the
@@ -1223,11 +1226,12 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // tid&15 of that row (16-byte chunks XOR-swizzled at load time).  bf16
   // sources go HBM -> LDS directly (global_load_lds_dwordx4: lane i of a
   // wavefront lands at byte 16*i of a 1 KiB stripe of 4 rows), so the next
-  // tile is in flight while the current one is consumed; E4M3FN pool bytes are
-  // loaded into registers, decoded, and written to LDS after the current tile's
-  // compute.  Rows past the valid keys are zero.
-  u32x2 kr[4], vr[4];  // E4M3FN tiles: raw code bytes, converted when committed to LDS
-  float ksr = 0.0f, vsr = 0.0f;
+  // tile is in flight while the current one is consumed.  E4M3FN pool bytes
+  // take the same route into the second half of the next tile's buffer (K
+  // codes, then V codes, 8 KiB each, unswizzled) and their scales straight to
+  // sm.u.pf.ks/vs; after the current tile's compute the workgroup decodes
+  // them into that buffer's bf16 K and V tiles (commit_tile).  Rows past the
+  // valid keys are zero.
   const int* prow = p.ptab + (int64_t)r * p.ptab_stride;
   const int npages = paged ? (kend + p.block_size - 1) / p.block_size : 0;
   const bool cached = npages <= MAX_PAGES;
@@ -1244,7 +1248,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     kgo[it] = row * krow + 8 * ((tid & 15) ^ (row & 15));
     vgo[it] = row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1));
   }
-  auto issue_tile = [&](int kv0, int buf) {
+  auto issue_tile = [&](int kv0, int buf) -> int {
     const int ntok = min(TT, kend - kv0);
     bool ok = true;
     int64_t slot0 = 0, kbase, vbase;  // element offsets of the tile's first key, head h
@@ -1268,24 +1272,25 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     if (fresh) ok = true;
     const int nv = ok ? ntok : 0;
     if (src_fp8) {
+      // All 64 rows of the tile's block are loaded (they lie in that block,
+      // block_size being a multiple of 64; without a valid block, rows of
+      // block 0 stand in): rows from nv on are zeroed when committed.
+      const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + (ok ? kbase : 0);
+      const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + (ok ? vbase : 0);
+      uint8_t* stg = (buf ? st1 : st0) + TILE_BYTES;
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int row = (tid >> 4) + 16 * it;
-        u32x2 kx = u32x2{0, 0}, vx = u32x2{0, 0};  // code 0 decodes to +0
-        if (row < nv) {
-          kx = ld8(static_cast<const uint8_t*>(p.k_cache) + kbase + kgo[it]);
-          vx = ld8(static_cast<const uint8_t*>(p.v_cache) + vbase + vgo[it]);
-        }
-        kr[it] = kx;
-        vr[it] = vx;
+      for (int it = 0; it < 2; ++it) {
+        const int q = it * NT + tid;  // 16-byte piece q: row q >> 3, bytes 16 * (q & 7)
+        const int off = (q >> 3) * krow + 16 * (q & 7);
+        const uint32_t dst = lds_addr(stg + 16 * (it * NT + wave * 64));
+        dma16(kc + off, dst);
+        dma16(vc + off, dst + 8192);
       }
-      if (tid < TT) {
-        const bool okt = tid < nv;
-        const int64_t si = (slot0 + tid) * p.hkv + h;
-        ksr = okt ? p.k_scale[si] : 0.0f;
-        vsr = okt ? p.v_scale[si] : 0.0f;
+      if (wave < 2) {
+        const float* sc = wave ? p.v_scale : p.k_scale;
+        dma4(sc + (ok ? (slot0 + lane) * p.hkv + h : 0), lds_addr(wave ? sm.u.pf.vs[buf] : sm.u.pf.ks[buf]));
       }
-      return;
+      return nv;
     }
     const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
     const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
@@ -1305,7 +1310,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
         dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
       }
-      return;
+      return nv;
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -1318,20 +1323,37 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
       }
     }
+    return nv;
   };
-  // Register-staged (E4M3FN) tiles only: the code bytes loaded by issue_tile
-  // (in flight during the current tile's compute) are decoded to bf16 here.
-  auto commit_tile = [&](int buf) {
+  // E4M3FN tiles only: once the codes and scales issued for buffer `buf` have
+  // landed, every thread decodes its 4 rows' K and V chunks (the swizzled bf16
+  // layout of the DMA path) into that buffer; the V tile overwrites the codes,
+  // so all of them are read before any is written.  Rows from nv on become
+  // zeros and their scales 0.
+  auto commit_tile = [&](int buf, int nv) {
     if (!src_fp8) return;
+    uint8_t* tb = buf ? st1 : st0;
+    const uint8_t* stg = tb + TILE_BYTES;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    u32x2 kx[4], vx[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
-      st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(kr[it]));
-      st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(vr[it]));
+      const bool okr = row < nv;
+      kx[it] = okr ? ld8(stg + row * HD + 8 * ((tid & 15) ^ (row & 15))) : u32x2{0, 0};
+      vx[it] = okr ? ld8(stg + 8192 + row * HD + 8 * ((tid & 15) ^ ((row & 7) << 1))) : u32x2{0, 0};
     }
-    if (tid < TT) {
-      sm.u.pf.ks[buf][tid] = ksr;
-      sm.u.pf.vs[buf][tid] = vsr;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      st16(tb + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(kx[it]));
+      st16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(vx[it]));
+    }
+    if (tid < TT && tid >= nv) {
+      sm.u.pf.ks[buf][tid] = 0.0f;
+      sm.u.pf.vs[buf][tid] = 0.0f;
     }
   };
 
@@ -1371,8 +1393,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
   }
   if (kstart < kstop) {
-    issue_tile(kstart, 0);
-    commit_tile(0);
+    const int nv0 = issue_tile(kstart, 0);
+    commit_tile(0, nv0);
   }
   // Each tile is processed as two halves of 32 keys,
   // software-pipelined so that MFMA work of one half and the softmax VALU
@@ -1402,7 +1424,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) kf[jj] = kread_h(0, jj);
     }
-    if (more) issue_tile(kv0 + TT, buf ^ 1);
+    const int nv1 = more ? issue_tile(kv0 + TT, buf ^ 1) : 0;
     if (active) {
       f32x4 s0[2][NQT], s1[2][NQT];
 #pragma unroll
@@ -1455,7 +1477,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 #pragma unroll
         for (int nt = 0; nt < NQT; ++nt) o[i][nt] = mfma16(vf[i], pb1[nt], o[i][nt]);
     }
-    if (more) commit_tile(buf ^ 1);
+    if (more) commit_tile(buf ^ 1, nv1);
   };
   // Tiles before the first one with a key past the valid rows or after the
   // block's first query position (bottom-right causal) need no mask.
@@ -1826,16 +1848,18 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
           // Split items only where the row splits (which implies 16-position
           // blocks); other items keep the tile loop compiled without the
           // split's range and merge code.
-          if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, item - sm.off[r], ltid, item, true);
-          else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          const int lr = item - sm.off[r];
+          if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
+          else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
+          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
         } else if constexpr (HAS_PF) {
+          // The row's items are 16-position blocks exactly when the item
+          // counts above took them so (tmr > split_tiles, E4M3FN launches).
+          const int lr = item - sm.off[r];
           int wr = 0, tr = 0;
           if constexpr (FP8) pf_work(p, r, wr, tr);
-          if (FP8 && tr > sm.split_tiles)
-            prefill_item<FP8, FP8 ? 1 : 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
-          else
-            prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, item - sm.off[r], ltid);
+          if (FP8 && tr > sm.split_tiles) prefill_item<FP8, FP8 ? 1 : 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
+          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
         }
         // The next item is fetched only now: fetching ahead would let a
         // workgroup claim a second item before a late-starting one takes its
