@@ -280,20 +280,22 @@ constexpr float RESCALE_LOG2 = 8.0f;
 // c = softmax_scale*log2(e), so e = exp2(c*s - c*m) is one FMA and one
 // v_exp_f32 per score; column reductions use v_permlane16/32_swap.  MASK
 // selects the boundary-tile path (keys past the tile's valid rows or causally
-// after the column).  Packs P^T into pb[nt] (the B operand of the half's PV
+// after the column).  SCALED (E4M3FN launches): scores take the keys' K scales
+// and probabilities their V scales from ks/vs (1.0 for tiles of bf16 rows),
+// without a per-score select.  Packs P^T into pb[nt] (the B operand of the half's PV
 // product) and returns in alpha[nt] the factor the accumulators must take
 // before that product; grow_any is set when any column's offset moved.
 // Branch-free for bf16 sources, so the compiler can interleave it with MFMA
 // work of the other half.
-template <int NQT, bool MASK>
+template <int NQT, bool MASK, bool SCALED>
 __device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT], float (&l)[NQT], float (&alpha)[NQT],
-                                             bool& grow_any, bf16x8 (&pb)[NQT], float c, bool src_fp8,
+                                             bool& grow_any, bf16x8 (&pb)[NQT], float c,
                                              const float* ks, const float* vs, int g, int ntok, int kh, int kv0,
                                              int lim0) {
   uint64_t grows = 0;
 #pragma unroll
   for (int nt = 0; nt < NQT; ++nt) {
-    if (src_fp8) {
+    if constexpr (SCALED) {
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) sh[mm][nt] *= *reinterpret_cast<const f32x4*>(ks + kh + 16 * mm + 4 * g);
     }
@@ -320,12 +322,13 @@ __device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT
     float rs = 0.0f;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const f32x4 vsc = src_fp8 ? *reinterpret_cast<const f32x4*>(vs + kh + 16 * mm + 4 * g) : f32x4{1, 1, 1, 1};
+      f32x4 vsc = f32x4{1, 1, 1, 1};
+      if constexpr (SCALED) vsc = *reinterpret_cast<const f32x4*>(vs + kh + 16 * mm + 4 * g);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float e = __builtin_amdgcn_exp2f(fmaf(sh[mm][nt][i], c, -cm));
         rs += e;
-        sh[mm][nt][i] = src_fp8 ? e * vsc[i] : e;
+        sh[mm][nt][i] = SCALED ? e * vsc[i] : e;
       }
     }
     rs = col_sum(rs);
@@ -1331,7 +1334,15 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // so all of them are read before any is written.  Rows from nv on become
   // zeros and their scales 0.
   auto commit_tile = [&](int buf, int nv) {
-    if (!src_fp8) return;
+    if (!src_fp8) {
+      // bf16 rows of an E4M3FN launch: unit scales (read after the next
+      // tile's barrier).
+      if (FP8 && tid < TT) {
+        sm.u.pf.ks[buf][tid] = 1.0f;
+        sm.u.pf.vs[buf][tid] = 1.0f;
+      }
+      return;
+    }
     uint8_t* tb = buf ? st1 : st0;
     const uint8_t* stg = tb + TILE_BYTES;
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -1447,7 +1458,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 #pragma unroll
         for (int nt = 0; nt < NQT; ++nt)
           s1[jj & 1][nt] = mfma16(as_bf16x8(kf[jj]), as_bf16x8(qv[nt][jj >> 1]), s1[jj & 1][nt]);
-      softmax_half<NQT, MASK>(s0, m, l, a0, g0, pb0, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
+      softmax_half<NQT, MASK, FP8>(s0, m, l, a0, g0, pb0, p.scale_log2, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
                             0, kv0, lim0);
       if (g0) {
 #pragma unroll
@@ -1462,7 +1473,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int nt = 0; nt < NQT; ++nt) o[i][nt] = mfma16(vf[i], pb0[nt], o[i][nt]);
-      softmax_half<NQT, MASK>(s1, m, l, a1, g1, pb1, p.scale_log2, src_fp8, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
+      softmax_half<NQT, MASK, FP8>(s1, m, l, a1, g1, pb1, p.scale_log2, sm.u.pf.ks[buf], sm.u.pf.vs[buf], g, ntok,
                             32, kv0, lim0);
       if (g1) {
 #pragma unroll
