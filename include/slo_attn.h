@@ -192,10 +192,12 @@ typedef struct slo_paged_attention_args {
   size_t workspace_bytes;
   int32_t phases;                 /* SLO_PHASE_* mask */
 
-  /* Optional KV write in the same launch (bf16 pools only), the store of
+  /* Optional KV write in the same launch, the store of
    * forward_mixed / Attention.forward (nanovllm/layers/mixed_attention.py:
    * 33, nanovllm/layers/attention.py:66-67) folded into the attention
-   * launch.  When store_slot_mapping is not NULL, new row t of new_k/new_v
+   * launch (with an E4M3FN pool: the quantising store of
+   * slo_store_kvcache with store_scale_floor, and at most 8 query heads per
+   * kv head).  When store_slot_mapping is not NULL, new row t of new_k/new_v
    * ([num_new_rows == num_q_rows, num_kv_heads, head_dim] bf16, contiguous:
    * row stride num_kv_heads * head_dim, 16-byte aligned; decode rows' tokens first,
    * then the prefill rows' tokens in cu_seqlens_q order) is written to pool
@@ -212,6 +214,7 @@ typedef struct slo_paged_attention_args {
   const void* new_v;
   int64_t new_v_row_stride;
   int32_t num_new_rows;
+  float store_scale_floor;  /* E4M3FN pools: scale_floor of the folded store (> 0) */
 } slo_paged_attention_args;
 
 /*

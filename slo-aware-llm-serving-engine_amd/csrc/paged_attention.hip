@@ -165,6 +165,7 @@ struct Params {
   int64_t nv_stride;
   int32_t nnew;
   int64_t num_slots;
+  float scale_floor;  // E4M3FN pools with the KV write folded in: the store's scale_floor
   // How long a split-K merge task waits for its chunks before it gives up
   // (s_memrealtime ticks).
   int64_t merge_wait_ticks;
@@ -273,6 +274,9 @@ __device__ __forceinline__ float col_sum(float x) {
 // from fp32 overflow in the row sum) and O is rescaled only on those rare
 // tiles.  The result o / l is the same quantity as with an exact running max.
 constexpr float RESCALE_LOG2 = 8.0f;
+// issue_tile's return value: valid rows, plus FRESH8 for an E4M3FN tile of new
+// tokens (folded KV write) that commit_tile makes from the new rows.
+constexpr int FRESH8 = 1024;
 
 // Online softmax of one half tile (32 keys: score blocks sh[0], sh[1] hold key
 // rows kh + 16*mm + 4g + i) for the wavefront's NQT query columns.  Scores stay
@@ -450,9 +454,10 @@ __device__ __forceinline__ constexpr int d_chunk() { return NSTEP * d_step<FP8>(
 template <bool FP8>
 __device__ __forceinline__ constexpr int d_chunk_min() { return d_chunk<FP8>() / 2; }  // two live steps
 // Vector memory operations per wavefront step: bf16 4 K + 4 V; E4M3FN 4 K
-// codes + 4 V codes + 1 of scales.
-template <bool FP8>
-__device__ __forceinline__ constexpr int d_group() { return FP8 ? 9 : 8; }
+// codes + 4 V codes + 1 of scales, and with the KV write folded in 1 of the
+// row's new K and V.
+template <bool FP8, bool FOLD>
+__device__ __forceinline__ constexpr int d_group() { return FP8 ? (FOLD ? 10 : 9) : 8; }
 
 // s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -625,8 +630,8 @@ __device__ __forceinline__ void decode_issue_q(const Params& p, uint8_t* qbuf, c
 // from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN (32 tokens):
 // see below; the scales go to `scl`.
 template <bool FP8, bool FOLD>
-__device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, float* scl, const DMeta& m, int s,
-                                             int wave, int lane) {
+__device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, float* scl, uint8_t* nrw, const DMeta& m,
+                                             int s, int wave, int lane) {
   const int n = lane & 15, g = lane >> 4;
   const int ntok = decode_ntok<FP8>(p, m, s, wave);
   const int t0 = m.tok0 + s * d_step<FP8>() + wave * d_dt<FP8>();
@@ -636,7 +641,7 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, floa
     const uint32_t dst = lds_addr(stg);
     if (lane == 0) {
 #pragma unroll
-      for (int i = 0; i < d_group<FP8>(); ++i) dma4(p.dlens, dst + 4 * i);
+      for (int i = 0; i < d_group<FP8, FOLD>(); ++i) dma4(p.dlens, dst + 4 * i);
     }
     return;
   }
@@ -681,6 +686,14 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, floa
     }
     const float* sc = (lane & 32) ? p.v_scale : p.k_scale;
     dma4(sc + (slot0 + (lane & 31)) * p.hkv + m.h, lds_addr(scl));
+    if constexpr (FOLD) {
+      // The row's new K (lanes 0-15) and V (lanes 16-31) of head h, bf16, to
+      // nrw: the newest token's slot is written only at the launch's end, so
+      // its codes are made from them (decode_wstep).  Every step loads them.
+      const uint16_t* src = ((lane & 16) ? p.nv + (int64_t)m.b * p.nv_stride : p.nk + (int64_t)m.b * p.nk_stride) +
+                            m.h * HD + 8 * (lane & 15);
+      if (lane < 32) dma16(src, lds_addr(nrw));
+    }
   }
 }
 
@@ -800,9 +813,33 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const
 
 // One wavefront step: 16 bf16 tokens, or 32 E4M3FN tokens as two halves of 16
 // (the second skipped when it holds no valid token).
-template <bool FP8>
-__device__ __forceinline__ void decode_wstep(const Params& p, uint8_t* stg, const float* scl, int ntok,
-                                             const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l, int lane) {
+template <bool FP8, bool FOLD>
+__device__ __forceinline__ void decode_wstep(const Params& p, uint8_t* stg, float* scl, const uint8_t* nrw, int ntok,
+                                             int tnew, const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l,
+                                             int lane) {
+  if constexpr (FP8 && FOLD) {
+    // With the KV write folded in, the row's newest token (row tnew of this
+    // step, when it holds it) gets the codes and scales the store writes, made
+    // here from its new K and V as slo_store_kvcache makes them (lanes 32-63
+    // repeat lanes 0-31).
+    if (tnew >= 0 && tnew < ntok) {
+      const u32x4 x = ld16(nrw + 16 * (lane & 31));
+      float f[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_bits_to_f32(x[j] & 0xffffu);
+        f[2 * j + 1] = bf16_bits_to_f32(x[j] >> 16);
+      }
+      float sc;
+      const u32x2 codes = e4m3_encode8<16>(f, p.scale_floor, sc);
+      if (lane < 32) {
+        const int isv = lane >> 4, c8 = lane & 15, rl = tnew & 15;
+        uint8_t* row = stg + (tnew >> 4) * 4096 + isv * 2048 + rl * 128;
+        *reinterpret_cast<u32x2*>(row + 16 * ((c8 >> 1) ^ (rl & 7)) + 8 * (c8 & 1)) = codes;
+        if (c8 == 0) scl[isv * 32 + tnew] = sc;
+      }
+    }
+  }
   if constexpr (FP8) {
     decode_step<FP8>(p, stg, scl, scl + 32, min(ntok, DT), qv, o, m, l, lane);
     if (ntok > DT) decode_step<FP8>(p, stg + 4096, scl + DT, scl + 32 + DT, ntok - DT, qv, o, m, l, lane);
@@ -940,7 +977,7 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
 // makes exactly tasks + workgroups fetches on it, and the workgroup making
 // the last one resets it.
 constexpr int STORE_ROWS = 4;  // new rows per store task
-template <bool STORE>
+template <bool FP8, bool STORE>
 __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int decode_base, int dchunk, int tid) {
   uint32_t* mctr = reinterpret_cast<uint32_t*>(p.ctrl) + (2 * NLIST + list) * CTRL_STRIDE;
   const int ngroups = STORE ? (p.nnew + STORE_ROWS - 1) / STORE_ROWS : 0;
@@ -982,9 +1019,28 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (dst[j] < 0) continue;
-          uint16_t* base = static_cast<uint16_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
-          *reinterpret_cast<u32x4*>(base + (dst[j] >> 1)) = x[j];
+          if constexpr (FP8) {
+            // The quantising store of slo_store_kvcache: the 16 lanes of one
+            // (token, kv head) vector (whole groups: pieces and the token are
+            // the same across them) share its amax.
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              f[2 * k] = bf16_bits_to_f32(x[j][k] & 0xffffu);
+              f[2 * k + 1] = bf16_bits_to_f32(x[j][k] >> 16);
+            }
+            float sc;
+            const u32x2 codes = e4m3_encode8<HD / 8>(f, p.scale_floor, sc);
+            if (dst[j] < 0) continue;
+            const int64_t e = dst[j] >> 1;  // element (= byte) offset slot * row + d
+            uint8_t* base = static_cast<uint8_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
+            *reinterpret_cast<u32x2*>(base + e) = codes;
+            if ((e % HD) == 0) const_cast<float*>((dst[j] & 1) ? p.v_scale : p.k_scale)[e / HD] = sc;
+          } else {
+            if (dst[j] < 0) continue;
+            uint16_t* base = static_cast<uint16_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
+            *reinterpret_cast<u32x4*>(base + (dst[j] >> 1)) = x[j];
+          }
         }
       }
       continue;
@@ -1066,7 +1122,15 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   uint8_t* sb = st1 + wave * WSTAGE;  // odd steps
   float* ca = sm.u.dec.sc[0][wave];   // E4M3FN scales of even and odd steps
   float* cb = sm.u.dec.sc[1][wave];
-  constexpr int GROUP = d_group<FP8>();
+  // E4M3FN with the KV write folded in: the row's new K and V rows of even
+  // and odd steps, in the Q buffer past the item's Q (at most 8 query heads
+  // per kv head, checked on the host).
+  uint8_t* na = qbuf + 2048 + wave * 512;
+  uint8_t* nb = qbuf + QBUF + 2048 + wave * 512;
+  auto tnew_of = [&](const DMeta& mm, int s) {
+    return decode_L(p, mm) - 1 - (mm.tok0 + s * d_step<FP8>() + wave * d_dt<FP8>());
+  };
+  constexpr int GROUP = d_group<FP8, FOLD>();
   const int hgp = (p.G + 3) >> 2;  // merge stores per wavefront and item
   auto item_of = [&](uint32_t rel) { return decode_base + dec_index(list, nlist, FP8 ? p.hkv : 1, (int)rel); };
 
@@ -1080,10 +1144,10 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   lds_sync();
   decode_meta_read<FP8>(cur, sm, 0, wave);
   decode_issue_q(p, qbuf, cur, wave, lane);
-  decode_issue<FP8, FOLD>(p, sa, ca, cur, 0, wave, lane);
+  decode_issue<FP8, FOLD>(p, sa, ca, na, cur, 0, wave, lane);
   for (int i = 0; i < hgp; ++i)
     if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
-  decode_issue<FP8, FOLD>(p, sb, cb, cur, 1, wave, lane);
+  decode_issue<FP8, FOLD>(p, sb, cb, nb, cur, 1, wave, lane);
   uint32_t f = 0;
   bool fetching = true;  // the fetch in flight is a real one
   if (tid == 0) f = atomic_add_ret(ctr, 1u);
@@ -1107,8 +1171,8 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
     float m = NEG_INF, l = 0.0f;
-    decode_wstep<FP8>(p, sa, ca, decode_ntok<FP8>(p, cur, 0, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, ca, cur, 2, wave, lane);
+    decode_wstep<FP8, FOLD>(p, sa, ca, na, decode_ntok<FP8>(p, cur, 0, wave), tnew_of(cur, 0), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sa, ca, na, cur, 2, wave, lane);
 
     // Step 1: (cur, 1) has landed, and with it prev's stores (every
     // wavefront's, after the barrier) and the fetch.  Wavefront 0 finds the
@@ -1137,8 +1201,8 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       }
       decode_meta_dma<FP8>(p, sm, nxt, (k + 1) & 1, lane);
     }
-    decode_wstep<FP8>(p, sb, cb, decode_ntok<FP8>(p, cur, 1, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sb, cb, cur, 3, wave, lane);
+    decode_wstep<FP8, FOLD>(p, sb, cb, nb, decode_ntok<FP8>(p, cur, 1, wave), tnew_of(cur, 1), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sb, cb, nb, cur, 3, wave, lane);
 
     // Step 2: (cur, 2) and nxt's metadata have landed; the broadcast is
     // visible after the barrier.
@@ -1156,15 +1220,17 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     }
     if (!has1) nxt = cur;  // no next item: its loads repeat the current item's
     decode_issue_q(p, qnxt, nxt, wave, lane);
-    if (!half) decode_wstep<FP8>(p, sa, ca, decode_ntok<FP8>(p, cur, 2, wave), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, ca, nxt, 0, wave, lane);
+    if (!half)
+      decode_wstep<FP8, FOLD>(p, sa, ca, na, decode_ntok<FP8>(p, cur, 2, wave), tnew_of(cur, 2), qv, o, m, l, lane);
+    decode_issue<FP8, FOLD>(p, sa, ca, na, nxt, 0, wave, lane);
 
     // Step 3: (cur, 3) has landed.
     wait_vm<GROUP + 1>(0);
-    if (!half) decode_wstep<FP8>(p, sb, cb, decode_ntok<FP8>(p, cur, 3, wave), qv, o, m, l, lane);
+    if (!half)
+      decode_wstep<FP8, FOLD>(p, sb, cb, nb, decode_ntok<FP8>(p, cur, 3, wave), tnew_of(cur, 3), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
-    decode_issue<FP8, FOLD>(p, sb, cb, nxt, 1, wave, lane);
+    decode_issue<FP8, FOLD>(p, sb, cb, nb, nxt, 1, wave, lane);
     fetching = fetching && has1;
     if (tid == 0) f = atomic_add_ret(ctr, fetching ? 1u : 0u);
     prev = cur;
@@ -1291,6 +1357,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     if (fresh) ok = true;
     const int nv = ok ? ntok : 0;
     if (src_fp8) {
+      // Tiles of new tokens (folded KV write) are made from the new rows at
+      // commit time.
+      if (fresh) return nv + FRESH8;
       // All 64 rows of the tile's block are loaded (they lie in that block,
       // block_size being a multiple of 64; without a valid block, rows of
       // block 0 stand in): rows from nv on are zeroed when committed.
@@ -1349,7 +1418,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // layout of the DMA path) into that buffer; the V tile overwrites the codes,
   // so all of them are read before any is written.  Rows from nv on become
   // zeros and their scales 0.
-  auto commit_tile = [&](int buf, int nv) {
+  auto commit_tile = [&](int buf, int nv, int kv0) {
+    const bool fresh8 = nv >= FRESH8;
+    nv &= FRESH8 - 1;
     if (!src_fp8) {
       // bf16 rows of an E4M3FN launch: unit scales (read after the next
       // tile's barrier).
@@ -1361,6 +1432,44 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
     uint8_t* tb = buf ? st1 : st0;
     const uint8_t* stg = tb + TILE_BYTES;
+    if (FOLD && fresh8) {
+      // New tokens of the folded KV write: codes and scales as the store
+      // makes them (the 16 threads of a tile row hold its 16 chunks), decoded
+      // to bf16 like pool codes.  Rows from nv on are zeros, their scales 0.
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int row = (tid >> 4) + 16 * it;
+        u32x4 kb = u32x4{0, 0, 0, 0}, vb = u32x4{0, 0, 0, 0};
+        if (row < nv) {
+          const int64_t t = qrow0 - prefix + kv0 + row;
+          const int ck = (tid & 15) ^ (row & 15), cv = (tid & 15) ^ ((row & 7) << 1);
+          const u32x4 xk = ld16(p.nk + t * p.nk_stride + (int64_t)h * HD + 8 * ck);
+          const u32x4 xv = ld16(p.nv + t * p.nv_stride + (int64_t)h * HD + 8 * cv);
+          float fk[8], fv[8];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            fk[2 * k] = bf16_bits_to_f32(xk[k] & 0xffffu);
+            fk[2 * k + 1] = bf16_bits_to_f32(xk[k] >> 16);
+            fv[2 * k] = bf16_bits_to_f32(xv[k] & 0xffffu);
+            fv[2 * k + 1] = bf16_bits_to_f32(xv[k] >> 16);
+          }
+          float ksc, vsc;
+          kb = fp8x8_to_bf16x8(e4m3_encode8<16>(fk, p.scale_floor, ksc));
+          vb = fp8x8_to_bf16x8(e4m3_encode8<16>(fv, p.scale_floor, vsc));
+          if ((tid & 15) == 0) {
+            sm.u.pf.ks[buf][row] = ksc;
+            sm.u.pf.vs[buf][row] = vsc;
+          }
+        }
+        st16(tb + row * ROWB + ((tid & 15) << 4), kb);
+        st16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4), vb);
+      }
+      if (tid < TT && tid >= nv) {
+        sm.u.pf.ks[buf][tid] = 0.0f;
+        sm.u.pf.vs[buf][tid] = 0.0f;
+      }
+      return;
+    }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     u32x2 kx[4], vx[4];
@@ -1411,9 +1520,25 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         if (page < 0 || page >= p.num_blocks) continue;
         const int64_t slot = (int64_t)page * p.block_size + jj % p.block_size;
         const uint16_t* src = (isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + (int64_t)h * HD + 8 * pc;
-        uint16_t* dst = static_cast<uint16_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) +
-                        slot * p.hkv * HD + (int64_t)h * HD + 8 * pc;
-        *reinterpret_cast<u32x4*>(dst) = ld16(src);
+        const int64_t e = slot * p.hkv * HD + (int64_t)h * HD + 8 * pc;
+        if constexpr (FP8) {
+          // E4M3FN: the store's codes and scale (16 lanes per vector, whole
+          // groups: a token's 32 pieces are consecutive).
+          const u32x4 x = ld16(src);
+          float f[8];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            f[2 * k] = bf16_bits_to_f32(x[k] & 0xffffu);
+            f[2 * k + 1] = bf16_bits_to_f32(x[k] >> 16);
+          }
+          float sc;
+          const u32x2 codes = e4m3_encode8<HD / 8>(f, p.scale_floor, sc);
+          *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) + e) = codes;
+          if (pc == 0) const_cast<float*>(isv ? p.v_scale : p.k_scale)[e / HD] = sc;
+        } else {
+          uint16_t* dst = static_cast<uint16_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) + e;
+          *reinterpret_cast<u32x4*>(dst) = ld16(src);
+        }
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // written before any DMA of this item reads them
       __syncthreads();
@@ -1421,7 +1546,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   }
   if (kstart < kstop) {
     const int nv0 = issue_tile(kstart, 0);
-    commit_tile(0, nv0);
+    commit_tile(0, nv0, kstart);
   }
   // Each tile is processed as two halves of 32 keys,
   // software-pipelined so that MFMA work of one half and the softmax VALU
@@ -1504,7 +1629,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
 #pragma unroll
         for (int nt = 0; nt < NQT; ++nt) o[i][nt] = mfma16(vf[i], pb1[nt], o[i][nt]);
     }
-    if (more) commit_tile(buf ^ 1, nv1);
+    if (more) commit_tile(buf ^ 1, nv1, kv0 + TT);
   };
   // Tiles before the first one with a key past the valid rows or after the
   // block's first query position (bottom-right causal) need no mask.
@@ -1909,7 +2034,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     if (tid == 0 && sm.item == count + wgs - 1u) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
   }
-  tail_tasks<FOLD>(p, sm, list, nlist, decode_base, dchunk, tid);
+  tail_tasks<FP8, FOLD>(p, sm, list, nlist, decode_base, dchunk, tid);
 
   // Rows that belong to no decode or prefill row (the capacity padding of a
   // captured step) get zeros, so every output row is defined.
@@ -1926,7 +2051,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 
 using AttnKernel = void (*)(Params);
 
-// The instantiations, indexed [fold][fp8][mode] (FOLD launches use bf16 pools).
+// The instantiations, indexed [fold][fp8][mode].
 AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
   static const AttnKernel table[2][2][3] = {
       {{paged_attention_kernel<false, MODE_MIXED>, paged_attention_kernel<false, MODE_PREFILL>,
@@ -1935,7 +2060,8 @@ AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
         paged_attention_kernel<true, MODE_DECODE>}},
       {{paged_attention_kernel<false, MODE_MIXED, true>, paged_attention_kernel<false, MODE_PREFILL, true>,
         paged_attention_kernel<false, MODE_DECODE, true>},
-       {nullptr, nullptr, nullptr}},
+       {paged_attention_kernel<true, MODE_MIXED, true>, paged_attention_kernel<true, MODE_PREFILL, true>,
+        paged_attention_kernel<true, MODE_DECODE, true>}},
   };
   return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
 }
@@ -2052,7 +2178,10 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   }
   const bool store = a->store_slot_mapping != nullptr;
   if (store) {
-    if (fp8) return fail(SLO_ERR_UNSUPPORTED, "paged_attention: the KV write in the launch needs a bf16 pool");
+    if (fp8 && !(a->store_scale_floor > 0.0f))
+      return fail(SLO_ERR_INVALID, "paged_attention: the E4M3FN KV write needs store_scale_floor > 0");
+    if (fp8 && a->num_heads > 8 * a->num_kv_heads)
+      return fail(SLO_ERR_UNSUPPORTED, "paged_attention: the E4M3FN KV write in the launch needs <= 8 query heads per kv head");
     if (!a->k_cache || !a->v_cache || a->num_blocks <= 0 || a->block_size <= 0)
       return fail(SLO_ERR_INVALID, "paged_attention: the KV write needs the pool");
     const int64_t row = (int64_t)a->num_kv_heads * HD;
@@ -2137,6 +2266,7 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   p.nk_stride = a->new_k_row_stride;
   p.nv_stride = a->new_v_row_stride;
   p.nnew = store ? a->num_new_rows : 0;
+  p.scale_floor = a->store_scale_floor;
   p.num_slots = (int64_t)a->num_blocks * a->block_size;
   // A merge task waits up to 200 ms for its chunks (a whole decode launch
   // takes well under a millisecond) before it gives up and reports it.
@@ -2160,8 +2290,11 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   // registers.
   const bool fp8_reads = fp8 && (do_dec || (do_pf && p.ptab != nullptr));
   const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
-  const AttnKernel kernel = attn_kernel(store, fp8_reads, mode);  // store implies a bf16 pool (checked above)
-  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[store ? 1 : 0][fp8_reads ? 1 : 0][mode];
+  // With the KV write folded in, the pool's format decides the instantiation
+  // (its store quantises); otherwise what the launch reads does.
+  const bool kfp8 = store ? fp8 : fp8_reads;
+  const AttnKernel kernel = attn_kernel(store, kfp8, mode);
+  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[store ? 1 : 0][kfp8 ? 1 : 0][mode];
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   void* kargs[] = {&p};
   if (hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid), dim3(NT), kargs, 0,

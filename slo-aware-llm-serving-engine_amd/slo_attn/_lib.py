@@ -57,6 +57,7 @@ class PagedAttentionArgs(ctypes.Structure):
         ("new_k", _c_void_p), ("new_k_row_stride", _c_int64),
         ("new_v", _c_void_p), ("new_v_row_stride", _c_int64),
         ("num_new_rows", _c_int32),
+        ("store_scale_floor", ctypes.c_float),
     ]
 
 

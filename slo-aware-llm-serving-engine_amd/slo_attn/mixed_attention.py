@@ -44,13 +44,21 @@ def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
     meta = context.mixed
     if not k_cache.numel() or not v_cache.numel():
         raise RuntimeError("mixed forward requires an allocated KV pool")
-    # The library's own store into a bf16 pool runs inside the attention
-    # launch when the new rows are contiguous (same result, one launch less);
-    # any other store_fn runs first.
-    fold = (store_fn is store_kvcache and k_scale is None and phases == _lib.PHASE_ALL
-            and foldable(k, v))
+    # The library's own store runs inside the attention launch when the new
+    # rows are contiguous (same result, one launch less); any other store_fn
+    # runs first.  An E4M3FN pool folds it into pure decode steps only (with at
+    # most 8 query heads per kv head): the launch then quantises each decode
+    # row's newest token itself (16 rows of 64-1,024 tokens: 25.3 us, against
+    # the store kernel and a 24.1 us launch).  With prefill rows the folded
+    # E4M3FN launch measured slower than the store kernel and the launch: rows
+    # reading the pool re-quantise their new tokens' tiles in every item (24
+    # decode rows and two chunks, one after a 1,024-token prefix: 108 against
+    # 72 us), and cold rows run in the E4M3FN instantiation, which spills
+    # registers (4 cold rows: 134 against 107 us).
+    fold = (store_fn is store_kvcache and phases == _lib.PHASE_ALL and foldable(k, v)
+            and (k_scale is None or (q.shape[1] <= 8 * k.shape[1] and not meta.num_prefill_tokens)))
     if fold:
-        check_store(k, v, k_cache, v_cache, context.slot_mapping)
+        check_store(k, v, k_cache, v_cache, context.slot_mapping, k_scale, v_scale)
     elif k_scale is None:
         store_fn(k, v, k_cache, v_cache, context.slot_mapping)
     else:

@@ -307,7 +307,8 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
                     k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                     phases: int = _lib.PHASE_ALL, out: torch.Tensor | None = None,
                     store_slot_mapping: torch.Tensor | None = None, new_k: torch.Tensor | None = None,
-                    new_v: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
+                    new_v: torch.Tensor | None = None, noalloc: bool = False,
+                    store_scale_floor: float = _lib.FP8_SCALE_FLOOR) -> torch.Tensor:
     """One ragged launch: decode rows ``q[:num_decode]``, then prefill rows.
 
     Decode row b attends to ``decode_lens[b]`` cached tokens through
@@ -317,11 +318,13 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
     or, with ``prefill_tables=None``, from the contiguous ``k``/``v`` rows
     starting at ``cu_k[r]``.  Returns ``out`` ``[q rows, num_heads, head_dim]``.
 
-    With ``store_slot_mapping`` (bf16 pools), the same launch also writes
-    ``new_k``/``new_v`` (one row per query row: decode tokens, then prefill
-    tokens) to their slots, the store of forward_mixed folded in, and reads the
-    step's new tokens from those rows; the result is the separate store
-    followed by the launch, bit for bit.
+    With ``store_slot_mapping``, the same launch also writes ``new_k``/``new_v``
+    (one row per query row: decode tokens, then prefill tokens) to their slots,
+    the store of forward_mixed folded in, and reads the step's new tokens from
+    those rows; the result is the separate store followed by the launch, bit
+    for bit.  With an E4M3FN pool the write is ``store_kvcache``'s quantising
+    store (``store_scale_floor``), the new tokens are read as its codes and
+    scales, and at most 8 query heads may share a kv head.
 
     ``noalloc=True`` launches through ``slo_paged_attention_noalloc``, which
     uses the library's static per-GPU scratch instead of this module's
@@ -397,9 +400,9 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
             args.v, args.v_row_stride = v.data_ptr(), v.stride(0)
             args.num_kv_rows = min(k.shape[0], v.shape[0])
     if store_slot_mapping is not None:
-        check_store(new_k, new_v, k_cache, v_cache, store_slot_mapping)
-        if code != _lib.KV_BF16:
-            raise ValueError("the KV write in the attention launch needs a bf16 pool")
+        check_store(new_k, new_v, k_cache, v_cache, store_slot_mapping, k_scale, v_scale)
+        if code != _lib.KV_BF16 and num_heads > 8 * num_kv_heads:
+            raise ValueError("the E4M3FN KV write in the attention launch needs <= 8 query heads per kv head")
         if new_k.shape[0] != T or new_k.shape[1] != num_kv_heads or new_k.shape[2] != head_dim:
             raise ValueError("new_k/new_v must hold one [num_kv_heads, head_dim] row per query row")
         args.k_cache, args.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
@@ -408,6 +411,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor | None, v_cache: torc
         args.new_k, args.new_k_row_stride = new_k.data_ptr(), new_k.stride(0)
         args.new_v, args.new_v_row_stride = new_v.data_ptr(), new_v.stride(0)
         args.num_new_rows = T
+        args.store_scale_floor = float(store_scale_floor)
     args.num_heads, args.num_kv_heads, args.head_dim = num_heads, num_kv_heads, head_dim
     args.softmax_scale = float(softmax_scale)
     args.phases = int(phases)

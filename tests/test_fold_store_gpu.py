@@ -1,4 +1,4 @@
-"""The KV write folded into the attention launch (bf16 pools).
+"""The KV write folded into the attention launch (bf16 and E4M3FN pools).
 
 ``forward_mixed`` and ``Attention.forward`` run the library's own store inside
 the attention launch: the launch writes the step's new K/V rows to their slots
@@ -41,6 +41,82 @@ def test_forward_mixed_folded_store_equals_store_then_attend(device, index):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(kc1.view(torch.int16), kc0.view(torch.int16))
     assert torch.equal(vc1.view(torch.int16), vc0.view(torch.int16))
+
+
+def _fp8_pools(w, device):
+    """E4M3FN codes and scales of the workload's bf16 pool, written by the store kernel."""
+    base_k, base_v = w.k_cache.to(device), w.v_cache.to(device)
+    nblk, bs, hkv, dh = base_k.shape
+    kc = torch.empty(nblk, bs, hkv, dh, dtype=torch.uint8, device=device)
+    vc = torch.empty_like(kc)
+    ks = torch.empty(nblk, bs, hkv, dtype=torch.float32, device=device)
+    vs = torch.empty_like(ks)
+    slots = torch.arange(nblk * bs, dtype=torch.int32, device=device)
+    store_kvcache(base_k.view(-1, hkv, dh), base_v.view(-1, hkv, dh), kc, vc, slots, ks, vs)
+    return kc, vc, ks, vs
+
+
+def _fp8_fold_matches_store_then_attend(device, meta, slots, q, k, v, pools, scale, history):
+    """The folded E4M3FN launch against the store kernel followed by the same
+    launch: outputs, codes and scales bit for bit."""
+    d = meta.num_decode
+    nr = (meta.prefill_cu_q.numel() - 1) if meta.num_prefill_tokens else 0
+    p1 = tuple(t.clone() for t in pools)
+
+    def launch(kc, vc, ks, vs, **store):
+        return paged_attention(
+            q, kc, vc, scale, num_kv_heads=k.shape[1], k_scale=ks, v_scale=vs, num_decode=d,
+            decode_lens=meta.decode_lens, decode_tables=meta.decode_tables, num_prefill=nr,
+            prefill_cu_q=meta.prefill_cu_q, prefill_cu_k=meta.prefill_cu_k, max_q=meta.max_q, max_k=meta.max_k,
+            prefill_tables=meta.prefill_tables if history else None, k=None if history else k[d:],
+            v=None if history else v[d:], **store)
+    store_kvcache(k, v, pools[0], pools[1], slots, pools[2], pools[3])
+    ref = launch(*pools)
+    got = launch(*p1, store_slot_mapping=slots, new_k=k, new_v=v)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    for a_, b_ in zip(p1, pools):
+        assert torch.equal(a_.view(torch.uint8), b_.view(torch.uint8))
+
+
+@pytest.mark.parametrize("index", [0, 1, 2, 3, 4])
+def test_folded_fp8_store_equals_store_then_attend(device, index):
+    # E4M3FN pool: the launch quantises the new rows as the store kernel does
+    # (decode rows' newest tokens, prefill tiles of new tokens, the tile that
+    # straddles a prefix, the write at the end) -- same codes, scales and
+    # outputs, bit for bit, as the store kernel followed by the launch; with
+    # the rows reading the pool (history) and, where the workload allows,
+    # without.  forward_mixed folds pure decode steps.
+    w = workloads.config(index)
+    d = workloads.to_device(w, device)
+    if w.num_decode:
+        reserve_workspace(device, w.num_decode, max(len(t) for t in w.decode_tables) * w.block_size, 32, 8, 128)
+    for history in ((True, False) if not w.has_history else (True,)):
+        _fp8_fold_matches_store_then_attend(device, d["meta"], d["slot_mapping"], d["q"], d["k"], d["v"],
+                                            _fp8_pools(w, device), w.scale, history)
+    if not w.prefill_q:  # a pure decode step: forward_mixed takes the folded launch
+        ctx = SimpleNamespace(mixed=d["meta"], slot_mapping=d["slot_mapping"])
+        p0, p1 = _fp8_pools(w, device), _fp8_pools(w, device)
+        ref = forward_mixed(d["q"], d["k"], d["v"], p0[0], p0[1], ctx, w.scale, _two_launch_store, p0[2], p0[3])
+        got = forward_mixed(d["q"], d["k"], d["v"], p1[0], p1[1], ctx, w.scale, store_kvcache, p1[2], p1[3])
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+        for a_, b_ in zip(p1, p0):
+            assert torch.equal(a_.view(torch.uint8), b_.view(torch.uint8))
+
+
+def test_folded_fp8_store_on_small_blocks_and_straddled_prefixes(device):
+    # 64-token blocks, prefixes inside a key tile (100, 700: the tile holding
+    # the prefix end is written to the pool by each item before it is read)
+    # and decode rows whose newest token sits at a 16/32-token step edge.
+    from attn_cases import Case
+    case = Case([31, 63, 300, 1000], [100, 700, 0], [45, 90, 33], bs=64, seed=21, kv_fp8=True)
+    kc, vc = case.cpu_pools()
+    codes, scales = case.fp8_pools(kc, vc)
+    pools = tuple(torch.from_numpy(x.copy()).to(device) for x in (*codes, *scales))
+    slots = torch.tensor(case.slots, dtype=torch.int32, device=device)
+    _fp8_fold_matches_store_then_attend(device, case.meta(device), slots, case.q.to(device), case.k.to(device),
+                                        case.v.to(device), pools, case.scale, True)
 
 
 def test_folded_store_skips_padding_slots_and_matches_explicit_launch(device):
@@ -128,8 +204,10 @@ def test_v0_branches_fold_the_store(device):
          block_tables=i32([[0, -1], [1, 2], [-1, -1]]))
 
 
-def test_fold_rejects_fp8_pool_and_bad_rows(device):
-    hq, hkv, dh, bs = 8, 2, 128, 256
+def test_fold_rejects_wide_fp8_groups_and_bad_rows(device):
+    # An E4M3FN pool with more than 8 query heads per kv head cannot carry the
+    # write (forward_mixed then runs the store kernel first).
+    hq, hkv, dh, bs = 16, 1, 128, 256
     q = torch.zeros(2, hq, dh, dtype=torch.bfloat16, device=device)
     k = torch.zeros(2, hkv, dh, dtype=torch.bfloat16, device=device)
     kc = torch.zeros(2, bs, hkv, dh, dtype=torch.uint8, device=device)
@@ -138,8 +216,11 @@ def test_fold_rejects_fp8_pool_and_bad_rows(device):
     tb = torch.tensor([[0], [1]], dtype=torch.int32, device=device)
     slots = torch.tensor([0, bs], dtype=torch.int32, device=device)
     with pytest.raises(ValueError):
-        paged_attention(q, kc, kc.clone(), 1.0, num_kv_heads=hkv, k_scale=sc, v_scale=sc, num_decode=2,
+        paged_attention(q, kc, kc.clone(), 1.0, num_kv_heads=hkv, k_scale=sc, v_scale=sc.clone(), num_decode=2,
                         decode_lens=dl, decode_tables=tb, store_slot_mapping=slots, new_k=k, new_v=k)
+    hq, hkv = 8, 2
+    q = torch.zeros(2, hq, dh, dtype=torch.bfloat16, device=device)
+    k = torch.zeros(2, hkv, dh, dtype=torch.bfloat16, device=device)
     kb = torch.zeros(2, bs, hkv, dh, dtype=torch.bfloat16, device=device)
     with pytest.raises(ValueError):
         paged_attention(q, kb, kb.clone(), 1.0, num_kv_heads=hkv, num_decode=2, decode_lens=dl, decode_tables=tb,
