@@ -322,7 +322,8 @@ def main():
     torch.cuda.empty_cache()
 
     traffic = load_profile_json("traffic_mixed_24decode_2x512chunk.json")
-    counters = load_profile_json("counters_paged_attention.json").get("prefill_3", {})
+    all_counters = load_profile_json("counters_paged_attention.json")
+    counters = all_counters.get("prefill_3", {})
 
     def traffic_of(kernel):
         return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic else None
@@ -365,11 +366,13 @@ def main():
             "kv_cache": "e4m3fn codes + fp32 scale per (token, kv head)",
             "step_us": round(t8_step, 2), "step_tokens_per_s": round(tokens / (t8_step * 1e-6), 1),
             "fused": hbm(fp8_fused_bytes, t8_fused, avg_launch_us=round(t8_fused, 2),
-                         algorithmic_bytes_per_launch=fp8_fused_bytes),
-            "decode": hbm(fp8_dec_bytes, t8_dec, avg_launch_us=round(t8_dec, 2), decode_kv_bytes=fp8_dec_bytes),
+                         algorithmic_bytes_per_launch=fp8_fused_bytes, traffic=traffic_of("fused_fp8")),
+            "decode": hbm(fp8_dec_bytes, t8_dec, avg_launch_us=round(t8_dec, 2), decode_kv_bytes=fp8_dec_bytes,
+                          traffic=traffic_of("decode_fp8")),
             "prefill": {"bound": "mfma", "avg_launch_us": round(t8_pre, 2),
                         "achieved": round(flops / (t8_pre * 1e-6) / 1e12, 1), "unit": "TFLOP/s",
-                        "frac": round(flops / (t8_pre * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+                        "frac": round(flops / (t8_pre * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                        "mfma_busy": all_counters.get("prefill_3_fp8", {}).get("mfma_busy")},
         },
         "tp2_rank": {
             "heads": [16, 4, 128], "workload": w2.name,
