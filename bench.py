@@ -321,6 +321,21 @@ def main():
     del st2
     torch.cuda.empty_cache()
 
+    # ---- 16 short decode rows (64-1024 tokens): a pure decode step (forward_mixed,
+    # KV write folded in) and the decode launch alone, both pool formats
+    w0 = workloads.config(0)
+    small = {"workload": w0.name, "decode_rows": w0.num_decode, "decode_context_sum": sum(w0.decode_lens)}
+    for fp8 in (False, True):
+        st0 = Step(w0, device, fp8=fp8)
+        t0_step, _ = graph_time(st0.step)
+        t0_dec, _ = graph_time(lambda i: st0.attn(i, _lib.PHASE_DECODE))
+        small["e4m3fn" if fp8 else "bf16"] = {
+            "step_us": round(t0_step, 2),
+            "decode": hbm(st0.decode_bytes(), t0_dec, avg_launch_us=round(t0_dec, 2), decode_kv_bytes=st0.decode_bytes()),
+        }
+        del st0
+        torch.cuda.empty_cache()
+
     traffic = load_profile_json("traffic_mixed_24decode_2x512chunk.json")
     all_counters = load_profile_json("counters_paged_attention.json")
     counters = all_counters.get("prefill_3", {})
@@ -379,6 +394,7 @@ def main():
             "fused": hbm(t2_bytes, t2_fused, avg_launch_us=round(t2_fused, 2), algorithmic_bytes_per_launch=t2_bytes),
             "decode": hbm(t2_dec_bytes, t2_dec, avg_launch_us=round(t2_dec, 2), decode_kv_bytes=t2_dec_bytes),
         },
+        "decode_short_rows": small,
         "roofline_qk_norm_rope_store": hbm(qk_bytes, t_qk, traffic=traffic_of("qk"), kernel="qk_norm_rope_store_kernel",
                                            algorithmic_bytes_per_launch=qk_bytes, avg_launch_us=round(t_qk, 2),
                                            tokens=tokens),

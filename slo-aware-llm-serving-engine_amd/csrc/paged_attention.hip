@@ -446,13 +446,13 @@ static_assert(4 * WSTAGE <= STAGE_BYTES, "decode stage must fit the tile stage")
 // same bytes as 16 bf16 tokens), so a wavefront keeps as many bytes in flight
 // as with bf16 and an item of four steps spans 512 tokens.
 template <bool FP8>
-__device__ __forceinline__ constexpr int d_dt() { return FP8 ? 2 * DT : DT; }  // tokens per wavefront step
+__host__ __device__ __forceinline__ constexpr int d_dt() { return FP8 ? 2 * DT : DT; }  // tokens per wavefront step
 template <bool FP8>
-__device__ __forceinline__ constexpr int d_step() { return 4 * d_dt<FP8>(); }  // tokens per workgroup step
+__host__ __device__ __forceinline__ constexpr int d_step() { return 4 * d_dt<FP8>(); }  // tokens per workgroup step
 template <bool FP8>
-__device__ __forceinline__ constexpr int d_chunk() { return NSTEP * d_step<FP8>(); }  // tokens per item
+__host__ __device__ __forceinline__ constexpr int d_chunk() { return NSTEP * d_step<FP8>(); }  // tokens per item
 template <bool FP8>
-__device__ __forceinline__ constexpr int d_chunk_min() { return d_chunk<FP8>() / 2; }  // two live steps
+__host__ __device__ __forceinline__ constexpr int d_chunk_min() { return d_chunk<FP8>() / 2; }  // two live steps
 // Vector memory operations per wavefront step: bf16 4 K + 4 V; E4M3FN 4 K
 // codes + 4 V codes + 1 of scales, and with the KV write folded in 1 of the
 // row's new K and V.
@@ -955,6 +955,61 @@ __device__ __forceinline__ void decode_final(const Params& p, int b, int h, int 
   if (tid == 0) __hip_atomic_fetch_add(&p.counters[b * p.hkv + h], -nch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// KV write of new-row pieces [first, end) (16-byte pieces, a new row's K
+// pieces then its V pieces): each copied to the row's slot (slots < 0 or past
+// the pool are skipped), all loads of the call first, then the stores; the
+// E4M3FN pool gets the quantising store of slo_store_kvcache.  Thread tid
+// takes pieces first + tid + j * NT (j < 4); with first a multiple of 16, the
+// 16 lanes of one (token, kv head) vector are whole groups.
+template <bool FP8>
+__device__ __forceinline__ void store_new_rows(const Params& p, int64_t first, int64_t end, int tid) {
+  const int row = p.hkv * HD;  // elements of one K (or V) row
+  const int per_tok = 2 * (row / 8);
+  for (int64_t i0 = first; i0 < end; i0 += 4 * NT) {
+    u32x4 x[4];
+    int64_t dst[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = i0 + tid + j * NT;
+      const int64_t t = i / per_tok;
+      const int pc = (int)(i % per_tok);
+      const bool isv = pc >= row / 8;
+      const int e = 8 * (isv ? pc - row / 8 : pc);
+      dst[j] = -1;
+      x[j] = u32x4{0, 0, 0, 0};
+      if (i < end) {
+        const int64_t slot = p.sslots[t];
+        x[j] = ld16((isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + e);
+        if (slot >= 0 && slot < p.num_slots) dst[j] = 2 * (slot * row + e) + (isv ? 1 : 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (FP8) {
+        // The 16 lanes of one (token, kv head) vector (whole groups: pieces
+        // and the token are the same across them) share its amax.
+        float f[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          f[2 * k] = bf16_bits_to_f32(x[j][k] & 0xffffu);
+          f[2 * k + 1] = bf16_bits_to_f32(x[j][k] >> 16);
+        }
+        float sc;
+        const u32x2 codes = e4m3_encode8<HD / 8>(f, p.scale_floor, sc);
+        if (dst[j] < 0) continue;
+        const int64_t e = dst[j] >> 1;  // element (= byte) offset slot * row + d
+        uint8_t* base = static_cast<uint8_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
+        *reinterpret_cast<u32x2*>(base + e) = codes;
+        if ((e % HD) == 0) const_cast<float*>((dst[j] & 1) ? p.v_scale : p.k_scale)[e / HD] = sc;
+      } else {
+        if (dst[j] < 0) continue;
+        uint16_t* base = static_cast<uint16_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
+        *reinterpret_cast<u32x4*>(base + (dst[j] >> 1)) = x[j];
+      }
+    }
+  }
+}
+
 // Tail tasks, taken by each workgroup once its items are done: first the KV
 // write of the launch's new tokens (when the launch carries it), then the
 // split-K merges.  Store task i of list l writes new rows [4g, 4g + 4) for
@@ -986,8 +1041,7 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
   const uint32_t count = nstore + (list < ntask ? (uint32_t)((ntask - list + nlist - 1) / nlist) : 0u);
   const uint32_t wgs = (uint32_t)((gridDim.x - list + nlist - 1) / nlist);
   if (count == 0) return;  // a list without tasks is not touched: its counter stays zero
-  const int row = p.hkv * HD;                     // elements of one K (or V) row
-  const int pieces = STORE_ROWS * 2 * (row / 8);  // 16-byte pieces of one store task
+  const int per_tok = 2 * (p.hkv * HD / 8);  // 16-byte pieces of one new row's K and V
   for (;;) {
     if (tid == 0) sm.item = atomicAdd(mctr, 1u);
     lds_sync();
@@ -998,51 +1052,9 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
       return;
     }
     if (STORE && rel < nstore) {
-      // Copy rows [4g, 4g + 4): all loads of the task first, then the stores.
-      const int t0 = STORE_ROWS * (list + (int)rel * nlist);
-      for (int i0 = 0; i0 < pieces; i0 += 4 * NT) {
-        u32x4 x[4];
-        int64_t dst[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = i0 + tid + j * NT;
-          const int t = t0 + i / (2 * (row / 8)), pc = i % (2 * (row / 8));
-          const bool isv = pc >= row / 8;
-          const int e = 8 * (isv ? pc - row / 8 : pc);
-          dst[j] = -1;
-          x[j] = u32x4{0, 0, 0, 0};
-          if (i < pieces && t < p.nnew) {
-            const int64_t slot = p.sslots[t];
-            x[j] = ld16((isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + e);
-            if (slot >= 0 && slot < p.num_slots) dst[j] = 2 * (slot * row + e) + (isv ? 1 : 0);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (FP8) {
-            // The quantising store of slo_store_kvcache: the 16 lanes of one
-            // (token, kv head) vector (whole groups: pieces and the token are
-            // the same across them) share its amax.
-            float f[8];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              f[2 * k] = bf16_bits_to_f32(x[j][k] & 0xffffu);
-              f[2 * k + 1] = bf16_bits_to_f32(x[j][k] >> 16);
-            }
-            float sc;
-            const u32x2 codes = e4m3_encode8<HD / 8>(f, p.scale_floor, sc);
-            if (dst[j] < 0) continue;
-            const int64_t e = dst[j] >> 1;  // element (= byte) offset slot * row + d
-            uint8_t* base = static_cast<uint8_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
-            *reinterpret_cast<u32x2*>(base + e) = codes;
-            if ((e % HD) == 0) const_cast<float*>((dst[j] & 1) ? p.v_scale : p.k_scale)[e / HD] = sc;
-          } else {
-            if (dst[j] < 0) continue;
-            uint16_t* base = static_cast<uint16_t*>(const_cast<void*>((dst[j] & 1) ? p.v_cache : p.k_cache));
-            *reinterpret_cast<u32x4*>(base + (dst[j] >> 1)) = x[j];
-          }
-        }
-      }
+      // Rows [4g, 4g + 4).
+      const int64_t t0 = STORE_ROWS * (list + (int)rel * nlist);
+      store_new_rows<FP8>(p, t0 * per_tok, min((int64_t)p.nnew, t0 + STORE_ROWS) * per_tok, tid);
       continue;
     }
     const int task = list + (int)(rel - nstore) * nlist;
@@ -1242,6 +1254,153 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   lds_sync();
   if (tid == 0 && due) atomic_add_noret(&p.counters[prev.b * p.hkv + prev.h], 1u);
+}
+
+// ------------------------------------------------------------ direct decode
+constexpr int DIRECT_ENTRIES = 32;  // block-table entries of a direct chunk (at most 1024 tokens)
+// Short decode-only launches: one workgroup per (row, chunk, kv head), no work
+// lists, no prologue over the batch.  Chunks are `ns` workgroup steps (two
+// in flight), up to 1024 tokens; the grid covers every chunk the tables can
+// hold (chunks past a row's length exit after reading its length), so it is
+// sized from shapes only.  Workgroup x takes group g = (x / (8 hkv)) * 8 +
+// x % 8 and kv head (x / 8) % hkv: the kv heads of one (row, chunk) run on one
+// XCD (x % 8), where they share the lines of the E4M3FN scale rows, and
+// groups g = c * nd + b put every row's first chunks at the front of the grid.
+// A row with several chunks merges them in the workgroup whose ticket
+// increment arrives last (records stored before the increment, merged in
+// chunk order, so the result does not depend on which one merges); the
+// launch leaves every ticket at zero.  With the KV write folded in, the first
+// workgroups also copy the new rows to their slots (nothing in the launch
+// reads those slots: a decode row's newest token comes from its new row).
+template <bool FP8, bool FOLD>
+__global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_cap, int ns) {
+  __shared__ Smem sm;
+  __shared__ int dmeta[1 + DIRECT_ENTRIES];  // row length, then the chunk's block-table entries
+  __shared__ __attribute__((aligned(16))) uint8_t stage0[4 * WSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stage1[4 * WSTAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[2 * QBUF];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int x = blockIdx.x;
+
+  // Once per workgroup, on every path (after the item's loads are issued
+  // where it has one): its share of the KV write (4 * NT pieces per
+  // workgroup) and of the zeros for query rows past every decode and prefill
+  // row.
+  auto side_work = [&]() {
+    bool any = false;
+    if constexpr (FOLD) {
+      const int64_t per_wg = 4 * NT, all = (int64_t)p.nnew * (2 * (p.hkv * HD / 8));
+      if ((int64_t)x * per_wg < all) {
+        store_new_rows<FP8>(p, (int64_t)x * per_wg, min(all, (int64_t)(x + 1) * per_wg), tid);
+        any = true;
+      }
+    }
+    const int64_t covered = (int64_t)p.q_off_prefill + (p.np_all > 0 ? max(p.cu_q_all[p.np_all], 0) : 0);
+    if (covered < p.num_q_rows) {
+      any = true;
+      const int per_row = p.hkv * p.G * HD / 8;
+      const int64_t pieces = (p.num_q_rows - covered) * per_row;
+      for (int64_t i = (int64_t)x * NT + tid; i < pieces; i += (int64_t)gridDim.x * NT) {
+        const int64_t row = covered + i / per_row;
+        *reinterpret_cast<u32x4*>(p.out + row * p.out_stride + 8 * (i % per_row)) = u32x4{0, 0, 0, 0};
+      }
+    }
+    return any;
+  };
+
+  const int grp = (x / (8 * p.hkv)) * 8 + x % 8;
+  if (grp >= nch_cap * p.nd) {
+    side_work();
+    return;
+  }
+  DMeta m;
+  m.c = grp / p.nd;
+  m.b = grp % p.nd;
+  m.h = (x / 8) % p.hkv;
+  m.dindex = (m.b * nch_cap + m.c) * p.hkv + m.h;
+  m.span = ns * d_step<FP8>();
+  m.tok0 = m.c * m.span;
+  // The row's length and the chunk's block-table entries (bf16: one per
+  // workgroup step; E4M3FN: one per step and wavefront, since a 128-token
+  // step may span two blocks of 64), and Q (it depends on the row and head
+  // only), in one round trip.
+  {
+    constexpr int PER = FP8 ? 4 : 1;
+    const int e = lane - 1;
+    const int tok = m.tok0 + (e / PER) * d_step<FP8>() + (e % PER) * d_dt<FP8>();
+    const int32_t* src = (e >= 0 && e < PER * ns)
+                             ? p.dtab + (int64_t)m.b * p.dtab_stride + min(tok / p.block_size, p.dtab_width - 1)
+                             : p.dlens + m.b;
+    if (wave == 0 && lane <= PER * ns) dma4(src, lds_addr(dmeta));
+  }
+  decode_issue_q(p, qbuf, m, wave, lane);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+  m.len = __builtin_amdgcn_readfirstlane(dmeta[0]);
+  const int nch = decode_nch(p, m);
+  if (m.c >= nch) {
+    side_work();
+    return;
+  }
+  // Steps past the row's end are not run.
+  const int nrun = max(1, min(ns, (decode_L(p, m) - m.tok0 + d_step<FP8>() - 1) / d_step<FP8>()));
+  // Step s as an item of one step (its first token, block and span), for the
+  // decode helpers.
+  auto step = [&](int s) {
+    DMeta ms = m;
+    ms.tok0 = m.tok0 + s * d_step<FP8>();
+    ms.span = d_step<FP8>();
+    ms.page[0] = __builtin_amdgcn_readfirstlane(dmeta[1 + (FP8 ? 4 * s + wave : s)]);
+    return ms;
+  };
+
+  // Steps alternate between the two stages, two in flight; every stage and
+  // its scales and new rows are private to the wavefront, so a step needs
+  // only its loads' wait (GROUP vector memory operations per step and
+  // wavefront).
+  constexpr int GROUP = d_group<FP8, FOLD>();
+  uint8_t* sa = stage0 + wave * WSTAGE;
+  uint8_t* sb = stage1 + wave * WSTAGE;
+  float* ca = sm.u.dec.sc[0][wave];
+  float* cb = sm.u.dec.sc[1][wave];
+  uint8_t* na = qbuf + 2048 + wave * 512;
+  uint8_t* nb = qbuf + QBUF + 2048 + wave * 512;
+  decode_issue<FP8, FOLD>(p, sa, ca, na, step(0), 0, wave, lane);
+  if (nrun > 1) decode_issue<FP8, FOLD>(p, sb, cb, nb, step(1), 0, wave, lane);
+  const bool side = side_work();  // its loads and stores are counted too: wait for all
+  const int n = lane & 15, g = lane >> 4;
+  u32x4 qv[4];
+  {
+    const int hn = min(n, p.G - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qbuf + hn * ROWB + 16 * (4 * kk + g));
+  }
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
+  float mx = NEG_INF, l = 0.0f;
+  const int L = decode_L(p, m);
+  for (int s = 0; s < nrun; ++s) {
+    const bool odd = s & 1;
+    if (s + 1 < nrun && !(s == 0 && side)) __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    const DMeta ms = step(s);
+    decode_wstep<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, decode_ntok<FP8>(p, ms, 0, wave),
+                            L - 1 - (ms.tok0 + wave * d_dt<FP8>()), qv, o, mx, l, lane);
+    if (s + 2 < nrun) decode_issue<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, step(s + 2), 0, wave, lane);
+  }
+  lds_sync();
+  decode_merge(p, sm, stage1, m, tid, o, mx, l);
+  if (nch == 1) return;
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this workgroup's records stored before its ticket
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = atomic_add_ret(&p.counters[m.b * p.hkv + m.h], 1u);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    sm.row = (int)after_wait(old) == nch - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (sm.row) decode_final(p, m.b, m.h, m.b * nch_cap * p.hkv + m.h, nch, tid);
 }
 
 // --------------------------------------------------------------- prefill item
@@ -2066,6 +2225,21 @@ AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
   return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
 }
 
+using DirectKernel = void (*)(Params, int, int);
+DirectKernel direct_kernel(bool fold, bool fp8) {
+  static const DirectKernel table[2][2] = {{decode_direct_kernel<false, false>, decode_direct_kernel<true, false>},
+                                           {decode_direct_kernel<false, true>, decode_direct_kernel<true, true>}};
+  return table[fold ? 1 : 0][fp8 ? 1 : 0];
+}
+// Decode-only launches whose direct grid of the longest chunks (one workgroup
+// per chunk the tables can hold) is at most this many times what the GPU
+// holds at once run the direct kernel (bf16, E4M3FN pools); longer launches
+// run the work lists.  Measured on rows of 64-8192 tokens: the direct kernel
+// wins up to these sizes (16 rows of 64-1024 tokens 30 -> 15 us, 24 rows of
+// 256-4096 53 -> 51 us bf16 and 41 -> 37 us E4M3FN), the work lists beyond.
+constexpr int DIRECT_MAX_ROUNDS[2] = {4, 2};
+constexpr int DIRECT_CHUNK_MAX = 1024;  // tokens
+
 // Compute units and, per instantiation, the workgroups one CU holds at once
 // (registers and LDS of that kernel), cached per device.  A persistent launch
 // of CUs x that many workgroups keeps every workgroup resident.
@@ -2073,6 +2247,7 @@ struct DeviceShape {
   int cus = 0;
   int wallclock_khz = 0;  // s_memrealtime rate
   int wg_per_cu[2][2][3] = {};
+  int wg_direct[2] = {};  // decode_direct_kernel (without the KV write), by pool format
 };
 
 int device_shape(DeviceShape* out) {
@@ -2098,6 +2273,12 @@ int device_shape(DeviceShape* out) {
             return fail(SLO_ERR_HIP, "occupancy query failed");
           s.wg_per_cu[fold][fp8][mode] = std::max(1, n);
         }
+    for (int fp8 = 0; fp8 < 2; ++fp8) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, direct_kernel(false, fp8), NT, 0) != hipSuccess)
+        return fail(SLO_ERR_HIP, "occupancy query failed");
+      s.wg_direct[fp8] = std::max(1, n);
+    }
     cache[dev] = s;
     ready[dev] = true;
   }
@@ -2295,6 +2476,24 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   const bool kfp8 = store ? fp8 : fp8_reads;
   const AttnKernel kernel = attn_kernel(store, kfp8, mode);
   const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[store ? 1 : 0][kfp8 ? 1 : 0][mode];
+  if (mode == MODE_DECODE) {
+    // The shortest chunks whose grid fits what the GPU holds at once; else
+    // the longest, when their grid fits DIRECT_MAX_ROUNDS times.
+    const int64_t held = (int64_t)ds.cus * ds.wg_direct[kfp8 ? 1 : 0];
+    const int step_tokens = kfp8 ? d_step<true>() : d_step<false>();
+    const int max_steps = DIRECT_CHUNK_MAX / step_tokens;
+    for (int steps = 2; steps <= max_steps; steps *= 2) {
+      const int ch = steps * step_tokens;
+      const int nch_cap = std::max(1, (dec_len_cap + ch - 1) / ch);
+      const int64_t dgrid = ((int64_t)p.nd * nch_cap + 7) / 8 * 8 * p.hkv;
+      if (dgrid > (steps == max_steps ? DIRECT_MAX_ROUNDS[kfp8 ? 1 : 0] * held : held)) continue;
+      void* dargs[] = {&p, const_cast<int*>(&nch_cap), &steps};
+      if (hipLaunchKernel(reinterpret_cast<const void*>(direct_kernel(store, kfp8)), dim3((unsigned)dgrid), dim3(NT),
+                          dargs, 0, static_cast<hipStream_t>(stream)) != hipSuccess)
+        return fail(SLO_ERR_HIP, "paged_attention: launch failed");
+      return check_launch("paged_attention");
+    }
+  }
   const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
   void* kargs[] = {&p};
   if (hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid), dim3(NT), kargs, 0,

@@ -92,6 +92,22 @@ def test_corrupt_old_values_are_detected(device):
         assert_close_gate(bad, expected)
 
 
+@pytest.mark.parametrize("kv_fp8", [False, True])
+@pytest.mark.parametrize("nd,cap,hq,hkv", [(4, 512, 32, 8), (16, 1024, 32, 8), (16, 2048, 32, 8), (24, 4096, 32, 8),
+                                           (16, 1024, 32, 2)])
+def test_direct_decode_chunk_lengths(device, kv_fp8, nd, cap, hq, hkv):
+    # Short decode-only launches run one workgroup per (row, chunk, kv head)
+    # with chunks of 2, 4, 8 or 16 workgroup steps (the shortest whose grid
+    # fits the GPU).  These shapes take each length on a 256-CU MI355X: rows
+    # of 1 token, one chunk plus one token, and the table's full width.
+    g = torch.Generator().manual_seed(nd * 31 + cap)
+    lens = torch.randint(1, cap + 1, (nd,), generator=g).tolist()
+    lens[0], lens[1], lens[2], lens[3] = cap, 1, 129, min(cap, 1025)
+    case = Case([L - 1 for L in lens], [], [], hq=hq, hkv=hkv, seed=nd + cap, kv_fp8=kv_fp8)
+    (mx, mn), _, _ = _check(case, device)
+    print(f"{nd} rows up to {cap} tokens, {hq}/{hkv} heads, fp8={kv_fp8}: max-abs {mx:.3e} mean-abs {mn:.3e}")
+
+
 # --------------------------------------------- benchmark configurations
 def _workload_case(index, kv_fp8=False, hq=32, hkv=8):
     from slo_attn import workloads
@@ -210,13 +226,16 @@ def test_deterministic_across_launches(device):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("index,kv_fp8", [(0, False), (3, False), (3, True), (4, False)])
-def test_merge_that_gives_up_is_reported_and_does_not_poison_the_next_launch(device, monkeypatch, index, kv_fp8):
+@pytest.mark.parametrize("index,kv_fp8,waits", [(0, False, False), (3, False, True), (3, True, True), (4, False, True)])
+def test_merge_that_gives_up_is_reported_and_does_not_poison_the_next_launch(device, monkeypatch, index, kv_fp8,
+                                                                            waits):
     # A split-K merge task waits a bounded time for the chunks of its (row, kv
     # head).  With the bound set to 0 from the host (SLO_ATTN_MERGE_WAIT_US),
     # tasks whose chunks are not all in give up at once: every kernel still
     # exits, the host's check raises, the tickets are back at zero, and the
     # next launch with the normal bound is bit-identical to an untouched one.
+    # Config 0 (16 short decode rows) runs the direct decode kernel, whose
+    # last-arriving chunk merges without waiting: the bound changes nothing.
     from slo_attn import check_workspaces, workspace_events
     case = _workload_case(index, kv_fp8)
     clean, _ = case.run_gpu(device)
@@ -232,7 +251,10 @@ def test_merge_that_gives_up_is_reported_and_does_not_poison_the_next_launch(dev
             assert "gave up waiting" in str(e), e
             gave_up += int(str(e).split("workspace_check: ")[1].split()[0])
     print(f"config {index} fp8={kv_fp8}: merges that gave up over 3 launches: {gave_up}")
-    assert gave_up > 0, "no merge task gave up: the bounded wait's exit did not run"
+    if waits:
+        assert gave_up > 0, "no merge task gave up: the bounded wait's exit did not run"
+    else:
+        assert gave_up == 0
     monkeypatch.delenv("SLO_ATTN_MERGE_WAIT_US")
     again, _ = case.run_gpu(device)
     check_workspaces()
