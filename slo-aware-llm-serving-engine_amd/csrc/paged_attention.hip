@@ -1262,10 +1262,13 @@ constexpr int DIRECT_ENTRIES = 32;  // block-table entries of a direct chunk (at
 // lists, no prologue over the batch.  Chunks are `ns` workgroup steps (two
 // in flight), up to 1024 tokens; the grid covers every chunk the tables can
 // hold (chunks past a row's length exit after reading its length), so it is
-// sized from shapes only.  Workgroup x takes group g = (x / (8 hkv)) * 8 +
-// x % 8 and kv head (x / 8) % hkv: the kv heads of one (row, chunk) run on one
-// XCD (x % 8), where they share the lines of the E4M3FN scale rows, and
-// groups g = c * nd + b put every row's first chunks at the front of the grid.
+// sized from shapes only.  Workgroup x takes kv head (x / 8) % hkv of group
+// g = j * 8 + (x + j) % 8, j = x / (8 hkv): the kv heads of one (row, chunk)
+// run on one XCD (x % 8), where they share the lines of the E4M3FN scale
+// rows; groups g = c * nd + b put every row's first chunks at the front of
+// the grid, and the rotation by j spreads a row's chunks over the XCDs (with
+// nd a multiple of 8, x % 8 alone would put every chunk of a row on one XCD:
+// 24 rows of 256-4096 tokens, 50.3 -> 45.5 us).
 // A row with several chunks merges them in the workgroup whose ticket
 // increment arrives last (records stored before the increment, merged in
 // chunk order, so the result does not depend on which one merges); the
@@ -1308,7 +1311,8 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
     return any;
   };
 
-  const int grp = (x / (8 * p.hkv)) * 8 + x % 8;
+  const int jx = x / (8 * p.hkv);
+  const int grp = jx * 8 + (x + jx) % 8;
   if (grp >= nch_cap * p.nd) {
     side_work();
     return;
