@@ -697,52 +697,30 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, floa
   }
 }
 
-// QK, online softmax and PV of one landed step into this wavefront's running
-// (o, m, l); lane (n, g) holds O^T[d = 16dt + 4g + i][head n] and the
-// statistics of head n.  Scores are in the log2 domain.
-template <bool FP8>
-__device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const float* ksp, const float* vsp, int ntok,
-                                            const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l, int lane) {
+// QK, online softmax and PV of one landed bf16 step (16 tokens) into this
+// wavefront's running (o, m, l); lane (n, g) holds O^T[d = 16dt + 4g + i][head
+// n] and the statistics of head n.  Scores are in the log2 domain.
+__device__ __forceinline__ void decode_step_bf16(const Params& p, const uint8_t* stg, int ntok, const u32x4 (&qv)[4],
+                                                 f32x4 (&o)[8], float& m, float& l, int lane) {
   const int n = lane & 15, g = lane >> 4;
-  uint8_t* vt = FP8 ? stg : stg + DT * ROWB;  // bf16 V tile (E4M3FN: decoded over the code bytes)
+  const uint8_t* vt = stg + DT * ROWB;
 
   // V^T operand: source lane n of group g reads row 4g + n/4, d = 16dt + 4(n%4).
-  const int r0 = 4 * g + (n >> 2);
-  // bf16: every LDS operand read of the step (4 K, 8 V^T fragments) is issued
+  // Every LDS operand read of the step (4 K, 8 V^T fragments) is issued
   // before the first MFMA, so the step pays one LDS round trip.
+  const int r0 = 4 * g + (n >> 2);
   s16x4 va[8];
-  if constexpr (!FP8) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
-  }
+  for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
   // S^T = K Q^T for the 16 tokens: k-step kk covers d = 32kk + 8g + {0..7}.
   u32x4 a[4];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    if constexpr (FP8) {
-      const int c = 2 * kk + (g >> 1);
-      a[kk] = fp8x8_to_bf16x8(ld8(stg + n * 128 + 16 * (c ^ (n & 7)) + 8 * (g & 1)));
-    } else {
-      a[kk] = ld16(stg + k_off(n, 4 * kk + g));
-    }
-  }
+  for (int kk = 0; kk < 4; ++kk) a[kk] = ld16(stg + k_off(n, 4 * kk + g));
   f32x4 s = f32x4{0, 0, 0, 0};
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) s = mfma16(as_bf16x8(a[kk]), as_bf16x8(qv[kk]), s);
 
-  if constexpr (FP8) {
-    // V codes -> bf16 tile over the code bytes: lane covers row lane/4, 32 bytes
-    // (d = 32*(lane%4)..+31).  All code reads of the wavefront are issued before
-    // its writes, and LDS executes a wavefront's accesses in order.
-    const int r = lane >> 2, seg = lane & 3;
-    u32x4 w0 = ld16(stg + 2048 + r * 128 + 16 * ((2 * seg) ^ (r & 7)));
-    u32x4 w1 = ld16(stg + 2048 + r * 128 + 16 * ((2 * seg + 1) ^ (r & 7)));
-    if (r >= ntok) w0 = w1 = u32x4{0, 0, 0, 0};
-    st16(vt + v_off(r, 4 * seg + 0), fp8x8_to_bf16x8(u32x2{w0.x, w0.y}));
-    st16(vt + v_off(r, 4 * seg + 1), fp8x8_to_bf16x8(u32x2{w0.z, w0.w}));
-    st16(vt + v_off(r, 4 * seg + 2), fp8x8_to_bf16x8(u32x2{w1.x, w1.y}));
-    st16(vt + v_off(r, 4 * seg + 3), fp8x8_to_bf16x8(u32x2{w1.z, w1.w}));
-  } else if (ntok < DT) {
+  if (ntok < DT) {
     // V rows past the valid tokens (whatever the pool holds there) become
     // zeros in the operand: lane (n, g) holds tokens 4g + {0..3}.
     const uint32_t m01 = (4 * g + 0 < ntok ? 0xffffu : 0u) | (4 * g + 1 < ntok ? 0xffff0000u : 0u);
@@ -754,18 +732,11 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const
     }
   }
 
-  f32x4 ksc = f32x4{1, 1, 1, 1}, vsc = f32x4{1, 1, 1, 1};
-  if constexpr (FP8) {
-    ksc = __builtin_bit_cast(f32x4, ld16(ksp + 4 * g));
-    vsc = __builtin_bit_cast(f32x4, ld16(vsp + 4 * g));
-  }
   float x[4];
   float mx = NEG_INF;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float v = s[i] * p.scale_log2;
-    if constexpr (FP8) v *= ksc[i];
-    x[i] = 4 * g + i < ntok ? v : NEG_INF;
+    x[i] = 4 * g + i < ntok ? s[i] * p.scale_log2 : NEG_INF;
     mx = fmaxf(mx, x[i]);
   }
   mx = col_max(mx);
@@ -780,9 +751,6 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const
   for (int i = 0; i < 4; ++i) {
     e[i] = __builtin_amdgcn_exp2f(x[i] - mu);
     rs += e[i];
-    // Scales of tokens past the valid ones are whatever the pool (or LDS)
-    // holds there: such a token's probability is 0 whatever its scale.
-    if constexpr (FP8) e[i] = 4 * g + i < ntok ? e[i] * vsc[i] : 0.0f;
   }
   rs = col_sum(rs);
   l = l * alpha + rs;
@@ -801,18 +769,105 @@ __device__ __forceinline__ void decode_step(const Params& p, uint8_t* stg, const
   const s16x4 pl = __builtin_bit_cast(s16x4, u32x2{
       pack_bf16x2(e[0] - __uint_as_float(h01 << 16), e[1] - __uint_as_float(h01 & 0xffff0000u)),
       pack_bf16x2(e[2] - __uint_as_float(h23 << 16), e[3] - __uint_as_float(h23 & 0xffff0000u))});
-  if constexpr (FP8) {  // the decoded tile is read only now
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) va[dt] = lds_tr16(vt + v_off(r0, 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3));
-  }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pb, o[dt], 0, 0, 0);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[dt], pl, o[dt], 0, 0, 0);
 }
 
-// One wavefront step: 16 bf16 tokens, or 32 E4M3FN tokens as two halves of 16
-// (the second skipped when it holds no valid token).
+// 8-byte transposed LDS read: lane (2j + c) of each 16-lane group passes the
+// address of bytes 8c..8c+7 of row j of an 8 x 16-byte block; lane n gets
+// byte n of rows 0..7 (byte j = row j).
+__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
+  typedef int v2i __attribute__((vector_size(8)));
+  const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(const_cast<uint8_t*>(p)));
+  return u32x2{(uint32_t)r[0], (uint32_t)r[1]};
+}
+
+// E4M3FN step of 32 tokens (the wavefront's codes: token t at half t / 16,
+// row t % 16 of stg, K codes at 4096 * half, V codes 2048 further; scales
+// ksp/vsp[t]).  The scores are made in two 16x16 products whose row r is
+// token 8 (r / 4) + 4h + r % 4 (half h), so lane (n, g) holds the scores of
+// tokens 8g..8g+7 of head n: one softmax update for the 32 tokens, and P^T
+// is the B operand of 16x16x32 products as it stands.  The V^T operand (row
+// d, tokens 8g..8g+7) comes straight from the codes by a transposed byte
+// read, masked to the valid tokens and converted in registers.
+__device__ __forceinline__ void decode_step_e4m3(const Params& p, const uint8_t* stg, const float* ksp,
+                                                 const float* vsp, int ntok, const u32x4 (&qv)[4], f32x4 (&o)[8],
+                                                 float& m, float& l, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  f32x4 s[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = 8 * (n >> 2) + 4 * h + (n & 3), rr = t & 15;
+    const uint8_t* kr = stg + (t >> 4) * 4096 + rr * 128;
+    u32x4 a[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = 2 * kk + (g >> 1);
+      a[kk] = fp8x8_to_bf16x8(ld8(kr + 16 * (c ^ (rr & 7)) + 8 * (g & 1)));
+    }
+    s[h] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) s[h] = mfma16(as_bf16x8(a[kk]), as_bf16x8(qv[kk]), s[h]);
+  }
+  // V^T fragments: lane (n, g) addresses row n / 2 (token 8g + n / 2), bytes
+  // 8 (n % 2).. of d-chunk dt.
+  const int tv = 8 * g + (n >> 1), rv = tv & 15;
+  const uint8_t* vr = stg + (tv >> 4) * 4096 + 2048 + rv * 128 + 8 * (n & 1);
+  u32x2 vc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) vc[dt] = lds_tr8(vr + 16 * (dt ^ (rv & 7)));
+  const f32x4 k0 = __builtin_bit_cast(f32x4, ld16(ksp + 8 * g)), k1 = __builtin_bit_cast(f32x4, ld16(ksp + 8 * g + 4));
+  const f32x4 v0 = __builtin_bit_cast(f32x4, ld16(vsp + 8 * g)), v1 = __builtin_bit_cast(f32x4, ld16(vsp + 8 * g + 4));
+  const int nv = min(max(ntok - 8 * g, 0), 8);  // valid tokens of this lane's 8
+  float x[8];
+  float mx = NEG_INF;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = i < nv ? s[0][i] * p.scale_log2 * k0[i] : NEG_INF;
+    x[4 + i] = 4 + i < nv ? s[1][i] * p.scale_log2 * k1[i] : NEG_INF;
+    mx = fmaxf(mx, fmaxf(x[i], x[4 + i]));
+  }
+  mx = col_max(mx);
+  const bool grow = mx - m > RESCALE_LOG2;  // false when both are -inf
+  const float mnew = grow ? mx : m;
+  const float mu = mnew == NEG_INF ? 0.0f : mnew;
+  const float alpha = grow ? __builtin_amdgcn_exp2f(m - mu) : 1.0f;
+  float e[8], rs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    e[i] = __builtin_amdgcn_exp2f(x[i] - mu);
+    rs += e[i];
+    // Scales of tokens past the valid ones are whatever LDS holds there.
+    e[i] = i < nv ? e[i] * (i < 4 ? v0[i] : v1[i - 4]) : 0.0f;
+  }
+  rs = col_sum(rs);
+  l = l * alpha + rs;
+  m = mnew;
+  if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+  }
+  u32x4 hi, lo;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t h2 = pack_bf16x2(e[2 * j], e[2 * j + 1]);
+    hi[j] = h2;
+    lo[j] = pack_bf16x2(e[2 * j] - __uint_as_float(h2 << 16), e[2 * j + 1] - __uint_as_float(h2 & 0xffff0000u));
+  }
+  // Codes of tokens past the valid ones may be NaN patterns: zeroed.
+  const uint64_t keep = nv >= 8 ? ~0ull : (1ull << (8 * nv)) - 1;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const uint32_t w0 = vc[dt].x & (uint32_t)keep, w1 = vc[dt].y & (uint32_t)(keep >> 32);
+    const u32x4 va = fp8x8_to_bf16x8(u32x2{w0, w1});
+    o[dt] = mfma16(as_bf16x8(va), as_bf16x8(hi), o[dt]);
+    o[dt] = mfma16(as_bf16x8(va), as_bf16x8(lo), o[dt]);
+  }
+}
+
+// One wavefront step: 16 bf16 tokens, or 32 E4M3FN tokens.
 template <bool FP8, bool FOLD>
 __device__ __forceinline__ void decode_wstep(const Params& p, uint8_t* stg, float* scl, const uint8_t* nrw, int ntok,
                                              int tnew, const u32x4 (&qv)[4], f32x4 (&o)[8], float& m, float& l,
@@ -841,10 +896,9 @@ __device__ __forceinline__ void decode_wstep(const Params& p, uint8_t* stg, floa
     }
   }
   if constexpr (FP8) {
-    decode_step<FP8>(p, stg, scl, scl + 32, min(ntok, DT), qv, o, m, l, lane);
-    if (ntok > DT) decode_step<FP8>(p, stg + 4096, scl + DT, scl + 32 + DT, ntok - DT, qv, o, m, l, lane);
+    decode_step_e4m3(p, stg, scl, scl + 32, ntok, qv, o, m, l, lane);
   } else {
-    decode_step<FP8>(p, stg, nullptr, nullptr, ntok, qv, o, m, l, lane);
+    decode_step_bf16(p, stg, ntok, qv, o, m, l, lane);
   }
 }
 
