@@ -321,6 +321,13 @@ def main():
     del st2
     torch.cuda.empty_cache()
 
+    traffic = load_profile_json("traffic_mixed_24decode_2x512chunk.json")
+    all_counters = load_profile_json("counters_paged_attention.json")
+    counters = all_counters.get("prefill_3", {})
+
+    def traffic_of(kernel):
+        return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic else None
+
     # ---- 16 short decode rows (64-1024 tokens): a pure decode step (forward_mixed,
     # KV write folded in) and the decode launch alone, both pool formats
     w0 = workloads.config(0)
@@ -331,17 +338,11 @@ def main():
         t0_dec, _ = graph_time(lambda i: st0.attn(i, _lib.PHASE_DECODE))
         small["e4m3fn" if fp8 else "bf16"] = {
             "step_us": round(t0_step, 2),
-            "decode": hbm(st0.decode_bytes(), t0_dec, avg_launch_us=round(t0_dec, 2), decode_kv_bytes=st0.decode_bytes()),
+            "decode": hbm(st0.decode_bytes(), t0_dec, avg_launch_us=round(t0_dec, 2), decode_kv_bytes=st0.decode_bytes(),
+                          traffic=traffic_of("decode0_fp8" if fp8 else "decode0"), kernel="decode_direct_kernel"),
         }
         del st0
         torch.cuda.empty_cache()
-
-    traffic = load_profile_json("traffic_mixed_24decode_2x512chunk.json")
-    all_counters = load_profile_json("counters_paged_attention.json")
-    counters = all_counters.get("prefill_3", {})
-
-    def traffic_of(kernel):
-        return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic else None
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(w)
     timing = f"HIP-graph replays of {NSETS} back-to-back launches over {NSETS} pool copies; us per launch"
@@ -370,7 +371,7 @@ def main():
                         algorithmic_bytes_per_launch=fused_bytes, avg_launch_us=round(t_fused, 2),
                         launches=n_fused, timing=timing),
         "roofline_decode": hbm(dec_bytes, t_dec, decode_kv_bytes=dec_bytes, traffic=traffic_of("decode"),
-                               avg_launch_us=round(t_dec, 2)),
+                               avg_launch_us=round(t_dec, 2), kernel="decode_direct_kernel"),
         "roofline_prefill": {
             "bound": "mfma", "achieved": round(pre_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(pre_tflops / BF16_PEAK_TFLOPS, 4), "flops": flops, "avg_launch_us": round(t_pre, 2),

@@ -1311,6 +1311,81 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
 }
 
 // ------------------------------------------------------------ direct decode
+// One chunk of a direct launch: nrun steps of item m (its block-table entries
+// at `entries`: one per step, E4M3FN one per step and wavefront), two in
+// flight, then the cross-wavefront merge and, with several chunks in the
+// row, the split-K merge by the chunk whose ticket increment arrives last
+// (records of chunk c of (row, head) at dfirst + c * hkv).  mid() runs once
+// after the first steps' loads are issued; it returns whether it issued
+// memory operations of its own (the first wait then covers everything).
+// Ends with LDS free for the next chunk.
+template <bool FP8, bool FOLD, typename Mid>
+__device__ __forceinline__ void run_chunk(const Params& p, Smem& sm, uint8_t* stage0, uint8_t* stage1, uint8_t* qbuf,
+                                          const int* entries, const DMeta& m, int nrun, int nch, int dfirst, int tid,
+                                          Mid&& mid) {
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Step s as an item of one step (its first token, block and span), for the
+  // decode helpers.
+  auto step = [&](int s) {
+    DMeta ms = m;
+    ms.tok0 = m.tok0 + s * d_step<FP8>();
+    ms.span = d_step<FP8>();
+    ms.page[0] = __builtin_amdgcn_readfirstlane(entries[FP8 ? 4 * s + wave : s]);
+    return ms;
+  };
+
+  // Steps alternate between the two stages, two in flight; every stage and
+  // its scales and new rows are private to the wavefront, so a step needs
+  // only its loads' wait (GROUP vector memory operations per step and
+  // wavefront).
+  constexpr int GROUP = d_group<FP8, FOLD>();
+  uint8_t* sa = stage0 + wave * WSTAGE;
+  uint8_t* sb = stage1 + wave * WSTAGE;
+  float* ca = sm.u.dec.sc[0][wave];
+  float* cb = sm.u.dec.sc[1][wave];
+  uint8_t* na = qbuf + 2048 + wave * 512;
+  uint8_t* nb = qbuf + QBUF + 2048 + wave * 512;
+  decode_issue<FP8, FOLD>(p, sa, ca, na, step(0), 0, wave, lane);
+  if (nrun > 1) decode_issue<FP8, FOLD>(p, sb, cb, nb, step(1), 0, wave, lane);
+  const bool side = mid();
+  const int n = lane & 15, g = lane >> 4;
+  u32x4 qv[4];
+  {
+    const int hn = min(n, p.G - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qbuf + hn * ROWB + 16 * (4 * kk + g));
+  }
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
+  float mx = NEG_INF, l = 0.0f;
+  const int L = decode_L(p, m);
+  for (int s = 0; s < nrun; ++s) {
+    const bool odd = s & 1;
+    if (s + 1 < nrun && !(s == 0 && side)) __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    const DMeta ms = step(s);
+    decode_wstep<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, decode_ntok<FP8>(p, ms, 0, wave),
+                            L - 1 - (ms.tok0 + wave * d_dt<FP8>()), qv, o, mx, l, lane);
+    if (s + 2 < nrun) decode_issue<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, step(s + 2), 0, wave, lane);
+  }
+  lds_sync();
+  decode_merge(p, sm, stage1, m, tid, o, mx, l);
+  if (nch > 1) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this workgroup's records stored before its ticket
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = atomic_add_ret(&p.counters[m.b * p.hkv + m.h], 1u);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      sm.row = (int)after_wait(old) == nch - 1 ? 1 : 0;
+    }
+    __syncthreads();
+    if (sm.row) decode_final(p, m.b, m.h, dfirst, nch, tid);
+  }
+  __syncthreads();
+}
+
+
 constexpr int DIRECT_ENTRIES = 32;  // block-table entries of a direct chunk (at most 1024 tokens)
 // Short decode-only launches: one workgroup per (row, chunk, kv head), no work
 // lists, no prologue over the batch.  Chunks are `ns` workgroup steps (two
@@ -1402,63 +1477,8 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
   }
   // Steps past the row's end are not run.
   const int nrun = max(1, min(ns, (decode_L(p, m) - m.tok0 + d_step<FP8>() - 1) / d_step<FP8>()));
-  // Step s as an item of one step (its first token, block and span), for the
-  // decode helpers.
-  auto step = [&](int s) {
-    DMeta ms = m;
-    ms.tok0 = m.tok0 + s * d_step<FP8>();
-    ms.span = d_step<FP8>();
-    ms.page[0] = __builtin_amdgcn_readfirstlane(dmeta[1 + (FP8 ? 4 * s + wave : s)]);
-    return ms;
-  };
-
-  // Steps alternate between the two stages, two in flight; every stage and
-  // its scales and new rows are private to the wavefront, so a step needs
-  // only its loads' wait (GROUP vector memory operations per step and
-  // wavefront).
-  constexpr int GROUP = d_group<FP8, FOLD>();
-  uint8_t* sa = stage0 + wave * WSTAGE;
-  uint8_t* sb = stage1 + wave * WSTAGE;
-  float* ca = sm.u.dec.sc[0][wave];
-  float* cb = sm.u.dec.sc[1][wave];
-  uint8_t* na = qbuf + 2048 + wave * 512;
-  uint8_t* nb = qbuf + QBUF + 2048 + wave * 512;
-  decode_issue<FP8, FOLD>(p, sa, ca, na, step(0), 0, wave, lane);
-  if (nrun > 1) decode_issue<FP8, FOLD>(p, sb, cb, nb, step(1), 0, wave, lane);
-  const bool side = side_work();  // its loads and stores are counted too: wait for all
-  const int n = lane & 15, g = lane >> 4;
-  u32x4 qv[4];
-  {
-    const int hn = min(n, p.G - 1);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qv[kk] = ld16(qbuf + hn * ROWB + 16 * (4 * kk + g));
-  }
-  f32x4 o[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
-  float mx = NEG_INF, l = 0.0f;
-  const int L = decode_L(p, m);
-  for (int s = 0; s < nrun; ++s) {
-    const bool odd = s & 1;
-    if (s + 1 < nrun && !(s == 0 && side)) __builtin_amdgcn_s_waitcnt(vmcnt_imm(GROUP));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    const DMeta ms = step(s);
-    decode_wstep<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, decode_ntok<FP8>(p, ms, 0, wave),
-                            L - 1 - (ms.tok0 + wave * d_dt<FP8>()), qv, o, mx, l, lane);
-    if (s + 2 < nrun) decode_issue<FP8, FOLD>(p, odd ? sb : sa, odd ? cb : ca, odd ? nb : na, step(s + 2), 0, wave, lane);
-  }
-  lds_sync();
-  decode_merge(p, sm, stage1, m, tid, o, mx, l);
-  if (nch == 1) return;
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this workgroup's records stored before its ticket
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t old = atomic_add_ret(&p.counters[m.b * p.hkv + m.h], 1u);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    sm.row = (int)after_wait(old) == nch - 1 ? 1 : 0;
-  }
-  __syncthreads();
-  if (sm.row) decode_final(p, m.b, m.h, m.b * nch_cap * p.hkv + m.h, nch, tid);
+  run_chunk<FP8, FOLD>(p, sm, stage0, stage1, qbuf, dmeta + 1, m, nrun, nch, m.b * nch_cap * p.hkv + m.h, tid,
+                       side_work);
 }
 
 // --------------------------------------------------------------- prefill item
