@@ -1593,10 +1593,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     if constexpr (FOLD) fresh = paged && kv0 >= prefix && qrow0 - prefix + kv0 + ntok <= p.nnew;
     if (fresh) ok = true;
     const int nv = ok ? ntok : 0;
-    if (src_fp8) {
-      // Tiles of new tokens (folded KV write) are made from the new rows at
-      // commit time.
-      if (fresh) return nv + FRESH8;
+    if (src_fp8 && !fresh) {
       // All 64 rows of the tile's block are loaded (they lie in that block,
       // block_size being a multiple of 64; without a valid block, rows of
       // block 0 stand in): rows from nv on are zeroed when committed.
@@ -1617,6 +1614,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       }
       return nv;
     }
+    // Tiles of new tokens in an E4M3FN launch (folded KV write): their bf16
+    // rows take this route too and are quantised in place at commit time.
+    const int ret = src_fp8 ? nv + FRESH8 : nv;
     const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
     const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
     if (fresh) {
@@ -1635,7 +1635,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
         dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
       }
-      return nv;
+      return ret;
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -1648,7 +1648,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
       }
     }
-    return nv;
+    return ret;
   };
   // E4M3FN tiles only: once the codes and scales issued for buffer `buf` have
   // landed, every thread decodes its 4 rows' K and V chunks (the swizzled bf16
@@ -1670,18 +1670,20 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     uint8_t* tb = buf ? st1 : st0;
     const uint8_t* stg = tb + TILE_BYTES;
     if (FOLD && fresh8) {
-      // New tokens of the folded KV write: codes and scales as the store
-      // makes them (the 16 threads of a tile row hold its 16 chunks), decoded
-      // to bf16 like pool codes.  Rows from nv on are zeros, their scales 0.
+      // New tokens of the folded KV write, landed as bf16 rows by this
+      // thread's own DMA (thread tid holds 16-byte slot tid & 15 of rows
+      // (tid >> 4) + 16 it; rows from nv on were zeroed): codes and scales as
+      // the store makes them (the 16 threads of a tile row hold its 16
+      // chunks), decoded back to bf16 in place.  Scales of rows from nv on
+      // are 0.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int row = (tid >> 4) + 16 * it;
         u32x4 kb = u32x4{0, 0, 0, 0}, vb = u32x4{0, 0, 0, 0};
         if (row < nv) {
-          const int64_t t = qrow0 - prefix + kv0 + row;
-          const int ck = (tid & 15) ^ (row & 15), cv = (tid & 15) ^ ((row & 7) << 1);
-          const u32x4 xk = ld16(p.nk + t * p.nk_stride + (int64_t)h * HD + 8 * ck);
-          const u32x4 xv = ld16(p.nv + t * p.nv_stride + (int64_t)h * HD + 8 * cv);
+          const u32x4 xk = ld16(tb + row * ROWB + ((tid & 15) << 4));
+          const u32x4 xv = ld16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4));
           float fk[8], fv[8];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
