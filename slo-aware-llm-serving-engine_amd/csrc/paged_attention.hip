@@ -255,11 +255,19 @@ __device__ __forceinline__ bf16x8 vt_operand(const uint8_t* tile, int ks, int dt
 
 // max / sum over the 4 lanes {l, l^16, l^32, l^48} (one query column) with
 // v_permlane16_swap / v_permlane32_swap instead of LDS-crossbar shuffles.
+// v_max_f32 without the canonicalising max(x, x) the compiler puts on each
+// operand of fmaxf that comes out of a lane swap (the scores are never NaN:
+// masked ones are -inf by selection).
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float col_max(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float col_sum(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
