@@ -1991,7 +1991,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 
   const int per = (nrows + NT - 1) / NT;  // rows per thread, at most 4
   const int r0 = tid * per;
-  const int nlist = min((int)gridDim.x, NLIST);
+  // The host launches at least NLIST workgroups (lists without items cost a
+  // workgroup nothing), so the list arithmetic is by a constant.
+  constexpr int nlist = NLIST;
   const int list = blockIdx.x % nlist;
 
 
@@ -2072,12 +2074,12 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     // measured best with a third of the work in prefill, a quarter with a
     // tenth.)
     if (tid == 0) {
-      int64_t permille = 500;
+      int permille = 500;
       if (MODE == MODE_MIXED) {
         const int64_t all = wt + 4 * dt * p.hkv;
-        if (all > 0) permille = min((int64_t)625, max((int64_t)250, 2000 * wt / all));
+        if (all > 0) permille = min(625, max(250, (int)(2000.0f * (float)wt / (float)all)));
       }
-      sm.pf_first = (int)((int64_t)gridDim.x * permille / 1000);
+      sm.pf_first = (int)(gridDim.x * (uint32_t)permille / 1000u);
       // Long decode launches (six items or more per workgroup): each list
       // cycles through the kv heads instead of keeping one.  Whole lists
       // otherwise finished up to 15% apart (the same heads always on the
@@ -2582,7 +2584,9 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
       return check_launch("paged_attention");
     }
   }
-  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(bound, slots));
+  // At least one workgroup per work list (the kernel's list arithmetic
+  // assumes NLIST lists).
+  const int grid = (int)std::max<int64_t>(NLIST, std::min<int64_t>(bound, slots));
   void* kargs[] = {&p};
   if (hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid), dim3(NT), kargs, 0,
                       static_cast<hipStream_t>(stream)) != hipSuccess)
