@@ -21,15 +21,17 @@ store_kvcache_kernel(const uint16_t* __restrict__ key, int64_t key_stride,
                      float* __restrict__ k_scale, float* __restrict__ v_scale,
                      int64_t num_slots, float scale_floor) {
   const int64_t tok = blockIdx.x;
-  const int64_t slot = slot_mapping[tok];
-  if (slot < 0 || slot >= num_slots) return;  // -1 marks a padded row
-  const int per = num_kv_heads * CPH;          // chunks per token per tensor
+  const int per = num_kv_heads * CPH;  // chunks per token per tensor
   const int64_t row_elems = (int64_t)num_kv_heads * CPH * 8;
   for (int c = threadIdx.x; c < 2 * per; c += blockDim.x) {
     const bool is_v = c >= per;
     const int cc = is_v ? c - per : c;
     const uint16_t* src = (is_v ? value + tok * value_stride : key + tok * key_stride) + cc * 8;
+    // The row's chunk and its slot load together (one round trip); a slot of
+    // -1 (a padded row) or past the pool skips the row.
     const u32x4 x = *reinterpret_cast<const u32x4*>(src);
+    const int64_t slot = slot_mapping[tok];
+    if (slot < 0 || slot >= num_slots) return;
     const int64_t dst = slot * row_elems + (int64_t)cc * 8;
     if (kv_dtype == KV_BF16) {
       uint16_t* cache = static_cast<uint16_t*>(is_v ? v_cache : k_cache);
