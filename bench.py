@@ -37,6 +37,10 @@ device synchronisations.
 * roofline_lm_head_argmax: the step after the model (LM head + greedy argmax
   fused, Qwen3-4B head 151936 x 2560 bf16) on the step's 26 sampled rows,
   against HBM (the weight read dominates).
+* roofline_decode.read_ceiling: what a plain read of the same byte count
+  achieves on this GPU (slo_attn/read_ceiling, a child process: one-pass
+  streams into VGPRs and through LDS-DMA, the decode kernels' route), and
+  the decode launch's rate as a fraction of the LDS-DMA stream.
 * cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
   step, median of 5 runs after 1 warm-up.
 """
@@ -46,6 +50,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -190,6 +195,19 @@ def hbm(bytes_, us, **extra):
     gbs = bytes_ / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), **extra}
+
+
+def read_ceiling(nbytes):
+    """Achievable read rates for nbytes: the read_ceiling program built next to
+    the library, run as a child process (None when it is not built or fails)."""
+    exe = os.path.join(ROOT, "slo-aware-llm-serving-engine_amd", "slo_attn", "read_ceiling")
+    if not os.path.exists(exe):
+        return None
+    try:
+        res = subprocess.run([exe, str(int(nbytes))], capture_output=True, text=True, timeout=120)
+        return json.loads(res.stdout.strip().splitlines()[-1]) if res.returncode == 0 else None
+    except (subprocess.TimeoutExpired, ValueError, IndexError):
+        return None
 
 
 def load_profile_json(name):
@@ -344,6 +362,10 @@ def main():
         del st0
         torch.cuda.empty_cache()
 
+    ceiling = read_ceiling(dec_bytes)
+    if ceiling:
+        ceiling["decode_frac_of_lds_dma_stream"] = round(
+            dec_bytes / (t_dec * 1e-6) / (ceiling["stream_lds_dma_TBps"] * 1e12), 4)
     cpu = None if args.no_cpu_baseline else cpu_baseline(w)
     timing = f"HIP-graph replays of {NSETS} back-to-back launches over {NSETS} pool copies; us per launch"
     line = {
@@ -371,7 +393,8 @@ def main():
                         algorithmic_bytes_per_launch=fused_bytes, avg_launch_us=round(t_fused, 2),
                         launches=n_fused, timing=timing),
         "roofline_decode": hbm(dec_bytes, t_dec, decode_kv_bytes=dec_bytes, traffic=traffic_of("decode"),
-                               avg_launch_us=round(t_dec, 2), kernel="decode_direct_kernel"),
+                               avg_launch_us=round(t_dec, 2), kernel="decode_direct_kernel",
+                               read_ceiling=ceiling),
         "roofline_prefill": {
             "bound": "mfma", "achieved": round(pre_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(pre_tflops / BF16_PEAK_TFLOPS, 4), "flops": flops, "avg_launch_us": round(t_pre, 2),
