@@ -2009,13 +2009,17 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // Item counts of this thread's rows under either choice (32-position
   // blocks / CHUNK, 16-position blocks / CHUNK_MIN), so the metadata is read
   // once.
-  int cnt_a[4], cnt_b[4], tmr[4];
+  // cnt_d holds the second count minus the first, so choosing a count is an
+  // addition: a choice between two array elements (alt ? cnt_b[i] : cnt_a[i])
+  // was compiled into a load through a selected address, which kept both
+  // arrays in scratch memory.
+  int cnt_a[4], cnt_d[4], tmr[4];
   {
     int w = 0, tm = 0, dn = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = r0 + i;
-      cnt_a[i] = cnt_b[i] = 0;
+      cnt_a[i] = cnt_d[i] = 0;
       tmr[i] = 0;
       if (i >= per || r >= nrows) continue;
       if (r < p.np) {
@@ -2026,12 +2030,12 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
         tmr[i] = tr;
         const int lq = p.cu_q[r + 1] - p.cu_q[r];
         cnt_a[i] = lq > 0 ? ((lq + 31) / 32) * p.hkv * p.HG : 0;
-        cnt_b[i] = lq > 0 ? ((lq + 15) / 16) * p.hkv * p.HG : 0;
+        cnt_d[i] = (lq > 0 ? ((lq + 15) / 16) * p.hkv * p.HG : 0) - cnt_a[i];
       } else {
         const int L = decode_len(p, r - p.np);
         dn += (L + d_chunk<FP8>() - 1) / d_chunk<FP8>();
         cnt_a[i] = max(1, (L + d_chunk<FP8>() - 1) / d_chunk<FP8>()) * p.hkv;
-        cnt_b[i] = max(1, (L + d_chunk_min<FP8>() - 1) / d_chunk_min<FP8>()) * p.hkv;
+        cnt_d[i] = max(1, (L + d_chunk_min<FP8>() - 1) / d_chunk_min<FP8>()) * p.hkv - cnt_a[i];
       }
     }
 
@@ -2103,7 +2107,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (i >= per || r0 + i >= nrows) continue;
-      const int c = bq == 16 ? cnt_b[i] : cnt_a[i];
+      const int c = cnt_a[i] + (bq == 16 ? cnt_d[i] : 0);
       base_c += c;
       if (pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) extra_c += c;
     }
@@ -2132,7 +2136,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == d_chunk_min<FP8>();
-    cnt[i] = alt ? cnt_b[i] : cnt_a[i];
+    cnt[i] = cnt_a[i] + (alt ? cnt_d[i] : 0);
     if (MODE == MODE_PREFILL && r0 + i < p.np && pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) cnt[i] *= 2;
     local_sum += cnt[i];
   }
