@@ -480,6 +480,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void dma16(const void* gp, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
 }
+// The same from a wave-uniform base plus a 32-bit per-lane byte offset (the
+// saddr form: the base stays in SGPRs, so a tile's loads need no per-lane
+// 64-bit address arithmetic).
+__device__ __forceinline__ void dma16_at(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+// A pointer that is the same in every lane, moved to SGPRs.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void dma4(const void* gp, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
 }
@@ -1571,12 +1585,14 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // (tid>>4)+16*it, swizzled 16-byte chunk) from the tile's first key.
   const int krow = paged ? p.hkv * HD : (int)p.k_stride;  // row strides < 2^25 elements (checked on the host)
   const int vrow = paged ? p.hkv * HD : (int)p.v_stride;
+  // FOLD: elements; otherwise bytes (row strides < 2^25 elements: 63 rows
+  // stay below 2^32 bytes), for the SGPR-base loads of issue_tile.
   int kgo[4], vgo[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int row = (tid >> 4) + 16 * it;
-    kgo[it] = row * krow + 8 * ((tid & 15) ^ (row & 15));
-    vgo[it] = row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1));
+    kgo[it] = (FOLD ? 1 : 2) * (row * krow + 8 * ((tid & 15) ^ (row & 15)));
+    vgo[it] = (FOLD ? 1 : 2) * (row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1)));
   }
   auto issue_tile = [&](int kv0, int buf) -> int {
     const int ntok = min(TT, kend - kv0);
@@ -1637,11 +1653,25 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     // which buffer a DMA writes); the loop waits for them explicitly.
     const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
     const uint32_t vdst = kdst + TILE_BYTES;
+    // Without the folded KV write the tile base goes to SGPRs and each load
+    // adds a 32-bit lane offset (prefill-only launches: config 1 105 -> 101
+    // us); the folded instantiation, short of SGPRs, keeps 64-bit lane
+    // addresses (its launch ran 1% slower with SGPR bases).
+    const void* kb = FOLD ? nullptr : uniform_ptr(ksrc);
+    const void* vb = FOLD ? nullptr : uniform_ptr(vsrc);
+    auto dma_k = [&](int it) {
+      if constexpr (FOLD) dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
+      else dma16_at(kb, (uint32_t)kgo[it], kdst + 16 * it * ROWB);
+    };
+    auto dma_v = [&](int it) {
+      if constexpr (FOLD) dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
+      else dma16_at(vb, (uint32_t)vgo[it], vdst + 16 * it * ROWB);
+    };
     if (nv == TT) {  // full tile: DMA only
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
-        dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
+        dma_k(it);
+        dma_v(it);
       }
       return ret;
     }
@@ -1649,8 +1679,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     for (int it = 0; it < 4; ++it) {
       const int row = (tid >> 4) + 16 * it;
       if (row < nv) {
-        dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
-        dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
+        dma_k(it);
+        dma_v(it);
       } else {
         st16((buf ? st1 : st0) + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
         st16((buf ? st1 : st0) + TILE_BYTES + row * ROWB + ((tid & 15) << 4), u32x4{0, 0, 0, 0});
