@@ -1608,8 +1608,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     int64_t slot0 = 0, kbase, vbase;  // element offsets of the tile's first key, head h
     if (paged && FOLD && kv0 < TT * 65536) {
       // The folded instantiation, short of SGPRs, finds the block without a
-      // division (config-3 folded launch 68.0 -> 67.4 us; the others ran
-      // slower this way).
+      // division (24 decode rows of 256-4096 tokens and two 512-token chunks:
+      // 68.0 -> 67.4 us; the other instantiations ran slower this way).
       const uint32_t t = (uint32_t)kv0 / TT;
       const int bi = tpb == 1 ? (int)t : (int)__umulhi(t, tpb_inv);  // t / tiles per block
       const int page = cached ? pages[bi] : prow[bi];
@@ -1673,7 +1673,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
     const uint32_t vdst = kdst + TILE_BYTES;
     // Without the folded KV write the tile base goes to SGPRs and each load
-    // adds a 32-bit lane offset (prefill-only launches: config 1 105 -> 101
+    // adds a 32-bit lane offset (four cold 1.1k-token prefill rows: 105 -> 101
     // us); the folded instantiation, short of SGPRs, keeps 64-bit lane
     // addresses (its launch ran 1% slower with SGPR bases).
     const void* kb = FOLD ? nullptr : uniform_ptr(ksrc);
