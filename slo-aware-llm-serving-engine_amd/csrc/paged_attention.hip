@@ -1509,12 +1509,7 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
 // (local index ((block * 2 + part) * hkv + h) * HG + hg, global `item`); each
 // writes (O, m, l) of its range as a record, and the one that arrives second
 // on the pair's ticket merges both and writes the output.
-// PAIRS (prefill-only launches): interior key tiles run in pairs, so each
-// tile's LDS buffer is a compile-time constant and its MFMA operand reads
-// take lane offsets plus immediates (three 512-token chunks after prefixes
-// 0/2048/512: about 71 -> 68 us, four cold 1.1k-token rows 96 -> 94.5 us;
-// mixed launches, timed once that way, showed no gain).
-template <bool FP8, int NQT, bool FOLD, bool SPLITK = false, bool PAIRS = false>
+template <bool FP8, int NQT, bool FOLD, bool SPLITK = false>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid,
                              int item = 0, bool split = false) {
   constexpr int BQ = 16 * NQT;
@@ -1938,11 +1933,13 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   const int n_int = lim_first < 0 ? 0 : lim_first / TT + 1;
   const int tfirst = kstart / TT;
   int kv0 = kstart, j = 0;
-  if constexpr (PAIRS) {
-    for (; kv0 + TT < kstop && tfirst + j + 1 < n_int; kv0 += 2 * TT, j += 2) {
-      tile(std::integral_constant<bool, false>(), kv0, 0);
-      tile(std::integral_constant<bool, false>(), kv0 + TT, 1);
-    }
+  // Interior tiles run in pairs, so each tile's LDS buffer is a constant and
+  // its MFMA operand reads take lane offsets plus immediates (three 512-token
+  // chunks after prefixes 0/2048/512, prefill-only: about 71 -> 68 us; 24
+  // decode rows of 256-4096 tokens and two 512-token chunks: 68.2 -> 67.5 us).
+  for (; kv0 + TT < kstop && tfirst + j + 1 < n_int; kv0 += 2 * TT, j += 2) {
+    tile(std::integral_constant<bool, false>(), kv0, 0);
+    tile(std::integral_constant<bool, false>(), kv0 + TT, 1);
   }
   for (; kv0 < kstop && tfirst + j < n_int; kv0 += TT, ++j) tile(std::integral_constant<bool, false>(), kv0, j);
   for (; kv0 < kstop; kv0 += TT, ++j) tile(std::integral_constant<bool, true>(), kv0, j);
@@ -2317,9 +2314,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
           // blocks); other items keep the tile loop compiled without the
           // split's range and merge code.
           const int lr = item - sm.off[r];
-          if (sp) prefill_item<FP8, 1, FOLD, true, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
-          else if (bq == 16) prefill_item<FP8, 1, FOLD, false, true>(p, sm, stage0, stage1, r, lr, ltid);
-          else prefill_item<FP8, 2, FOLD, false, true>(p, sm, stage0, stage1, r, lr, ltid);
+          if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
+          else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
+          else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
         } else if constexpr (HAS_PF) {
           // The row's items are 16-position blocks exactly when the item
           // counts above took them so (tmr > split_tiles, E4M3FN launches).
