@@ -41,12 +41,24 @@ def hipcc() -> str:
     return path
 
 
+# Kernels whose every instantiation must keep its registers out of scratch
+# memory (a spill there puts per-lane memory traffic into the tile loops).
+NO_SCRATCH = {"paged_attention.hip"}
+
+
 def _compile(src: str, obj: str) -> None:
-    cmd = [hipcc(), *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if src in NO_SCRATCH else []
+    cmd = [hipcc(), *FLAGS, *extra, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed on {src}")
+    if extra:
+        spills = [ln for ln in res.stderr.splitlines()
+                  if "ScratchSize [bytes/lane]:" in ln and not ln.rstrip().split("ScratchSize [bytes/lane]:")[1]
+                  .split()[0] == "0"]
+        if spills:
+            raise RuntimeError(f"{src}: a kernel instantiation uses scratch memory:\n" + "\n".join(spills))
 
 
 def build(jobs: int = 4) -> str:

@@ -38,12 +38,18 @@
 //    go from HBM straight into LDS (global_load_lds) and two steps stay in
 //    flight per wavefront across item boundaries.  The 4 wavefronts merge in
 //    LDS; a row with several chunks writes one (acc, m, l) record per chunk
-//    and increments the (row, kv head) ticket; the workgroup whose increment
-//    completes the count merges the records (the split-K merge of
-//    docs/project_manual.md:643-650) once its own items are done.  No
-//    workgroup ever waits for another, so the launch is correct whatever the
-//    number of workgroups resident at once.  After their items, workgroups
-//    take the folded KV write's store tasks from their list.
+//    and increments the (row, kv head) ticket.  After their items,
+//    workgroups take tail tasks from their list: the folded KV write's
+//    stores, and one merge task per (row, kv head), which waits until the
+//    ticket counts every chunk and then merges the records (the split-K
+//    merge of docs/project_manual.md:643-650).  That wait assumes every
+//    workgroup of the launch is resident at once (the grid is the
+//    instantiation's occupancy times the CUs); it is bounded (200 ms, or
+//    SLO_ATTN_MERGE_WAIT_US), and a task that gives up writes NaN to its
+//    outputs and counts the event, which slo_attention_workspace_check
+//    reports.  Decode-only launches that fit a few rounds of workgroups run
+//    decode_direct_kernel instead, where the workgroup whose chunk completes
+//    a ticket merges: no workgroup waits for another there.
 //
 // LDS tiles are 64 rows of 256 bytes with the 16-byte chunks of each row
 // XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 2*(row & 7)), so the MFMA
@@ -71,15 +77,14 @@
 #include <mutex>
 #include "common.h"
 #include "capi_internal.h"
+#include "tile_io.h"
 
 namespace slo {
 
-constexpr int HD = 128;                // head_dim this kernel implements
 constexpr int NT = 256;                // threads per workgroup (4 wavefronts)
 constexpr int TT = 64;                 // tokens per tile
 constexpr int CHUNK = 256;             // decode split-K chunk (tokens): four workgroup steps
 constexpr int CHUNK_MIN = 128;         // chunk of launches with few decode tokens (two live steps)
-constexpr int ROWB = HD * 2;           // bytes of one bf16 tile row
 constexpr int TILE_BYTES = TT * ROWB;  // 16 KiB
 constexpr int BQ_MIN = 16;             // query positions per prefill item: 16 or 32 (per launch)
 constexpr int MAX_ROWS = 1024;         // decode + prefill rows per launch
@@ -210,71 +215,6 @@ struct Smem {
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
 };
 
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
-__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
-
-// Byte offset of 16-byte chunk `c` of tile row `r` (K and V swizzles).
-__device__ __forceinline__ int k_off(int r, int c) { return r * ROWB + ((c ^ (r & 15)) << 4); }
-__device__ __forceinline__ int v_off(int r, int c) { return r * ROWB + ((c ^ ((r & 7) << 1)) << 4); }
-
-__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(const u32x2& w) {
-  const u32x2 a = fp8x4_to_bf16x4(w.x), b = fp8x4_to_bf16x4(w.y);
-  u32x4 r;
-  r.x = a.x;
-  r.y = a.y;
-  r.z = b.x;
-  r.w = b.y;
-  return r;
-}
-
-__device__ __forceinline__ s16x4 lds_tr16(const uint8_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(const_cast<uint8_t*>(p)));
-}
-
-__device__ __forceinline__ bf16x8 join_tr(const s16x4& a, const s16x4& b) {
-  const u32x2 x = __builtin_bit_cast(u32x2, a), y = __builtin_bit_cast(u32x2, b);
-  u32x4 r;
-  r.x = x.x;
-  r.y = x.y;
-  r.z = y.x;
-  r.w = y.y;
-  return as_bf16x8(r);
-}
-
-// V^T as the A operand of O^T = V^T P^T for k-step `ks` (32 tokens) and
-// d-tile `dt`: lane (n, g) receives d = 16dt + n of tokens 32ks + 4g + {0..3}
-// (slots 0-3) and 32ks + 16 + 4g + {0..3} (slots 4-7).
-__device__ __forceinline__ bf16x8 vt_operand(const uint8_t* tile, int ks, int dt, int g, int n) {
-  const int r0 = 32 * ks + 4 * g + (n >> 2);
-  const int c = 2 * dt + ((n & 3) >> 1);
-  const int half = (n & 1) << 3;
-  return join_tr(lds_tr16(tile + v_off(r0, c) + half), lds_tr16(tile + v_off(r0 + 16, c) + half));
-}
-
-// max / sum over the 4 lanes {l, l^16, l^32, l^48} (one query column) with
-// v_permlane16_swap / v_permlane32_swap instead of LDS-crossbar shuffles.
-// v_max_f32 without the canonicalising max(x, x) the compiler puts on each
-// operand of fmaxf that comes out of a lane swap (the scores are never NaN:
-// masked ones are -inf by selection).
-__device__ __forceinline__ float vmax(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float col_max(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float col_sum(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
 
 // The running max used as the exponent offset moves only when a tile's max
 // exceeds it by more than 2^RESCALE_LOG2 (in units of the log2-scaled score),
@@ -282,9 +222,6 @@ __device__ __forceinline__ float col_sum(float x) {
 // from fp32 overflow in the row sum) and O is rescaled only on those rare
 // tiles.  The result o / l is the same quantity as with an exact running max.
 constexpr float RESCALE_LOG2 = 8.0f;
-// issue_tile's return value: valid rows, plus FRESH8 for an E4M3FN tile of new
-// tokens (folded KV write) that commit_tile makes from the new rows.
-constexpr int FRESH8 = 1024;
 
 // Online softmax of one half tile (32 keys: score blocks sh[0], sh[1] hold key
 // rows kh + 16*mm + 4g + i) for the wavefront's NQT query columns.  Scores stay
@@ -407,6 +344,26 @@ __device__ __forceinline__ bool pf_splits(const Params& p, int r, int tiles, int
   const PfRow g = pf_row(p, r);
   return g.prefix >= g.Lq;
 }
+// Prefill-only launches order their prefill items by the key count of the
+// item's block, largest first, across rows: units (row, u) of hkv * HG items
+// each (u = the row's block index counted from its heaviest block, times two
+// with the halves of split rows) are ranked on the GPU.  Row geometry for the
+// ranking: {prefix, Lq, usable keys, nqb | mult << 16}.
+constexpr int PF_SORT_ROWS = 128;       // rows up to which the units are ranked
+constexpr int PF_SORT_UNITS = 1024;     // units up to which they are ranked
+constexpr int PF_SORT_COST = 1 << 14;   // units x rows up to which they are ranked
+// Blocks of a row whose key count (min(Lk, max(0, prefix + min(bq (b + 1),
+// Lq))), growing with b) exceeds K.
+__device__ __forceinline__ int pf_blocks_above(const int4& g, int bq, int K) {
+  const int nb = g.w & 0xffff;
+  if (nb == 0) return 0;
+  if (K < 0) return nb;
+  if (g.z <= K || g.x + g.y <= K) return 0;
+  const int x = K - g.x;
+  if (x < 0) return nb;
+  return max(0, nb - x / bq);
+}
+
 __device__ __forceinline__ float load_partial(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -466,82 +423,6 @@ __host__ __device__ __forceinline__ constexpr int d_chunk_min() { return d_chunk
 // row's new K and V.
 template <bool FP8, bool FOLD>
 __device__ __forceinline__ constexpr int d_group() { return FP8 ? (FOLD ? 10 : 9) : 8; }
-
-// s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9 encoding).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// LDS byte address of a pointer into a __shared__ array (wave-uniform).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
-}
-
-// global -> LDS DMA: lane i's 16 (or 4) bytes at gp land at LDS lds + 16i (4i).
-__device__ __forceinline__ void dma16(const void* gp, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
-}
-// The same from a wave-uniform base plus a 32-bit per-lane byte offset (the
-// saddr form: the base stays in SGPRs, so a tile's loads need no per-lane
-// 64-bit address arithmetic).
-__device__ __forceinline__ void dma16_at(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-// A pointer that is the same in every lane, moved to SGPRs.
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-  const uint64_t a = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-__device__ __forceinline__ void dma4(const void* gp, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
-}
-// Atomic add returning the old value; the value is valid only after a wait
-// that covers this operation.
-__device__ __forceinline__ uint32_t atomic_add_ret(void* p, uint32_t v) {
-  uint32_t r;
-  asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(r) : "v"(p), "v"(v) : "memory");
-  return r;
-}
-__device__ __forceinline__ void atomic_add_noret(void* p, uint32_t v) {
-  asm volatile("global_atomic_add %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-// Stores: agent-scope (write-through to the coherence point) for split-K
-// partials, plain for outputs.
-__device__ __forceinline__ void store16_agent(void* p, const u32x4& v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store16(void* p, const u32x4& v) {
-  asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store8(void* p, const u32x2& v) {
-  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store8_agent(void* p, const u32x2& v) {
-  asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void store4(void* p, uint32_t v) {
-  asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-// Ties x to this point: uses of x cannot move above an earlier wait.
-__device__ __forceinline__ uint32_t after_wait(uint32_t x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
-// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits
-// for every LDS DMA write still in flight (vmcnt), which would drain the KV
-// loads; the decode stages are private to their wavefront, so the barriers of
-// the decode loop (Q, merge area, item broadcast) need only the LDS counter.
-// The empty asm statements keep the compiler from moving memory accesses
-// across the barrier.
-__device__ __forceinline__ void lds_sync() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 struct DMeta {
   int b, h, c, dindex;  // wave-uniform
@@ -1152,9 +1033,9 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
       if (!ok) {
         // The chunks did not all arrive in time (workgroups of this launch
         // could not run: the GPU is shared, or the grid exceeds what it
-        // holds).  No merge: the outputs of (b, h) stay unwritten and the
-        // event counter reports it to the host.  The ticket still drops by
-        // nch, so the late increments bring it back to zero.
+        // holds).  No merge: the outputs of (b, h) are set to NaN below and
+        // the event counter reports it to the host.  The ticket still drops
+        // by nch, so the late increments bring it back to zero.
         __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(p.ctrl) + EVENTS_OFFSET / 4 + EV_MERGE_GAVE_UP, 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_fetch_add(ticket, 0u - nch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1164,7 +1045,17 @@ __device__ void tail_tasks(const Params& p, Smem& sm, int list, int nlist, int d
     lds_sync();
     const bool mine = __builtin_amdgcn_readfirstlane(sm.row) != 0;
     lds_sync();
-    if (mine) decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, (int)nch, tid);
+    if (mine) {
+      decode_final(p, b, h, sm.off[p.np + b] - decode_base + h, (int)nch, tid);
+    } else {
+      // NaN (bf16 0x7fc0) in every output of (b, h), so a consumer that does
+      // not check the workspace sees invalid values rather than stale ones.
+      for (int u = tid; u < p.G * (HD / 2); u += NT) {
+        const int hn = u / (HD / 2), d = 2 * (u % (HD / 2));
+        *reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_stride + (int64_t)(h * p.G + hn) * HD + d) =
+            0x7fc07fc0u;
+      }
+    }
   }
 }
 
@@ -1512,6 +1403,7 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
 template <bool FP8, int NQT, bool FOLD, bool SPLITK = false>
 __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, int r, int local, int tid,
                              int item = 0, bool split = false) {
+  static_assert(!(FP8 && FOLD), "E4M3FN launches with prefill rows run the store kernel first");
   constexpr int BQ = 16 * NQT;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -1657,9 +1549,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       }
       return nv;
     }
-    // Tiles of new tokens in an E4M3FN launch (folded KV write): their bf16
-    // rows take this route too and are quantised in place at commit time.
-    const int ret = src_fp8 ? nv + FRESH8 : nv;
+    const int ret = nv;
     const uint16_t* ksrc = (paged ? static_cast<const uint16_t*>(p.k_cache) : p.k) + kbase;
     const uint16_t* vsrc = (paged ? static_cast<const uint16_t*>(p.v_cache) : p.v) + vbase;
     if (fresh) {
@@ -1713,8 +1603,6 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // so all of them are read before any is written.  Rows from nv on become
   // zeros and their scales 0.
   auto commit_tile = [&](int buf, int nv, int kv0) {
-    const bool fresh8 = nv >= FRESH8;
-    nv &= FRESH8 - 1;
     if (!src_fp8) {
       // bf16 rows of an E4M3FN launch: unit scales (read after the next
       // tile's barrier).
@@ -1726,46 +1614,6 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
     uint8_t* tb = buf ? st1 : st0;
     const uint8_t* stg = tb + TILE_BYTES;
-    if (FOLD && fresh8) {
-      // New tokens of the folded KV write, landed as bf16 rows by this
-      // thread's own DMA (thread tid holds 16-byte slot tid & 15 of rows
-      // (tid >> 4) + 16 it; rows from nv on were zeroed): codes and scales as
-      // the store makes them (the 16 threads of a tile row hold its 16
-      // chunks), decoded back to bf16 in place.  Scales of rows from nv on
-      // are 0.
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int row = (tid >> 4) + 16 * it;
-        u32x4 kb = u32x4{0, 0, 0, 0}, vb = u32x4{0, 0, 0, 0};
-        if (row < nv) {
-          const u32x4 xk = ld16(tb + row * ROWB + ((tid & 15) << 4));
-          const u32x4 xv = ld16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4));
-          float fk[8], fv[8];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            fk[2 * k] = bf16_bits_to_f32(xk[k] & 0xffffu);
-            fk[2 * k + 1] = bf16_bits_to_f32(xk[k] >> 16);
-            fv[2 * k] = bf16_bits_to_f32(xv[k] & 0xffffu);
-            fv[2 * k + 1] = bf16_bits_to_f32(xv[k] >> 16);
-          }
-          float ksc, vsc;
-          kb = fp8x8_to_bf16x8(e4m3_encode8<16>(fk, p.scale_floor, ksc));
-          vb = fp8x8_to_bf16x8(e4m3_encode8<16>(fv, p.scale_floor, vsc));
-          if ((tid & 15) == 0) {
-            sm.u.pf.ks[buf][row] = ksc;
-            sm.u.pf.vs[buf][row] = vsc;
-          }
-        }
-        st16(tb + row * ROWB + ((tid & 15) << 4), kb);
-        st16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4), vb);
-      }
-      if (tid < TT && tid >= nv) {
-        sm.u.pf.ks[buf][tid] = 0.0f;
-        sm.u.pf.vs[buf][tid] = 0.0f;
-      }
-      return;
-    }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     u32x2 kx[4], vx[4];
@@ -1817,24 +1665,8 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
         const int64_t slot = (int64_t)page * p.block_size + jj % p.block_size;
         const uint16_t* src = (isv ? p.nv + t * p.nv_stride : p.nk + t * p.nk_stride) + (int64_t)h * HD + 8 * pc;
         const int64_t e = slot * p.hkv * HD + (int64_t)h * HD + 8 * pc;
-        if constexpr (FP8) {
-          // E4M3FN: the store's codes and scale (16 lanes per vector, whole
-          // groups: a token's 32 pieces are consecutive).
-          const u32x4 x = ld16(src);
-          float f[8];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            f[2 * k] = bf16_bits_to_f32(x[k] & 0xffffu);
-            f[2 * k + 1] = bf16_bits_to_f32(x[k] >> 16);
-          }
-          float sc;
-          const u32x2 codes = e4m3_encode8<HD / 8>(f, p.scale_floor, sc);
-          *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) + e) = codes;
-          if (pc == 0) const_cast<float*>(isv ? p.v_scale : p.k_scale)[e / HD] = sc;
-        } else {
-          uint16_t* dst = static_cast<uint16_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) + e;
-          *reinterpret_cast<u32x4*>(dst) = ld16(src);
-        }
+        uint16_t* dst = static_cast<uint16_t*>(const_cast<void*>(isv ? p.v_cache : p.k_cache)) + e;
+        *reinterpret_cast<u32x4*>(dst) = ld16(src);
       }
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // written before any DMA of this item reads them
       __syncthreads();
@@ -2043,6 +1875,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t stage1[STAGE_BYTES];
   // decode: Q of the current and next item
   __shared__ __attribute__((aligned(16))) uint8_t qbuf[HAS_DEC ? 2 * QBUF : 16];
+  // Prefill-only launches: the ranked units and the rows' geometry.
+  constexpr bool PF_SORT = MODE == MODE_PREFILL;
+  __shared__ uint32_t pf_units[PF_SORT ? PF_SORT_UNITS : 1];
+  __shared__ int4 pf_geo[PF_SORT ? PF_SORT_ROWS : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nrows = p.np + p.nd;
 
@@ -2216,6 +2052,53 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   __syncthreads();
   const int total = sm.off[nrows];
   const int decode_base = sm.off[p.np];
+  // Prefill-only launches: rank the units by their block's key count (ties:
+  // lower row, then lower u, so the two halves of a split block stay adjacent
+  // and item + hkv * HG is the second half of item).  Items are numbered in
+  // that order instead of row by row, so every row's heaviest items start
+  // first (four cold rows of 267-1,843 tokens: a later row's heaviest items
+  // otherwise waited for the lighter items of the rows before it).
+  const int per_unit = p.hkv * p.HG;
+  bool sorted = false;
+  if constexpr (PF_SORT) {
+    // Launches that split rows keep the row order: there the first round of
+    // workgroups pairs each CU's light item with a heavy half (two
+    // 512-token chunks after prefixes 0 and 1,024: 37 us in row
+    // order, 41 us ranked, where every CU started two heavy halves at once).
+    const int units = decode_base / per_unit;
+    sorted = p.np <= PF_SORT_ROWS && units <= PF_SORT_UNITS && (int64_t)units * p.np <= PF_SORT_COST &&
+             sm.pf_split_thr == (1 << 30);
+    if (sorted) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + i;
+        if (i >= per || r >= p.np) continue;
+        const PfRow g = pf_row(p, r);
+        const int nqb = g.Lq > 0 ? (g.Lq + bq - 1) / bq : 0;
+        const int mult = pf_splits(p, r, tmr[i], sm.pf_split_thr) ? 2 : 1;
+        pf_geo[r] = int4{g.prefix, g.Lq, g.Lk, nqb | (mult << 16)};
+      }
+      __syncthreads();
+      for (int r = 0; r < p.np; ++r) {
+        const int4 g = pf_geo[r];
+        const int nqb = g.w & 0xffff, mult = g.w >> 16;
+        for (int u = tid; u < nqb * mult; u += NT) {
+          const int b = nqb - 1 - u / mult;
+          const int K = min(g.z, max(0, g.x + min(bq * (b + 1), g.y)));
+          int rank = u - mult * pf_blocks_above(g, bq, K);
+          for (int r2 = 0; r2 < p.np; ++r2) {
+            const int4 g2 = pf_geo[r2];
+            const int m2 = g2.w >> 16;
+            const int above = pf_blocks_above(g2, bq, K);
+            rank += m2 * above;
+            if (r2 < r) rank += m2 * (pf_blocks_above(g2, bq, K - 1) - above);
+          }
+          pf_units[rank] = ((uint32_t)r << 16) | (uint32_t)u;
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // Work lists.  Prefill items [0, decode_base) and decode items
   // [decode_base, total) form two families; item i of a family belongs to list
@@ -2287,6 +2170,7 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       if (rel >= count) return -1;
       const int item =
           fam ? fbase + dec_index(list, nlist, FP8 ? p.hkv : 1, (int)rel) : fbase + list + (int)rel * nlist;
+      if (PF_SORT && sorted && !fam) return (int)(pf_units[item / per_unit] >> 16);
       for (int r = tid; r < nrows; r += NT)
         if (sm.off[r] <= item && item < sm.off[r + 1]) sm.row = r;
       __syncthreads();
@@ -2313,7 +2197,8 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
           // Split items only where the row splits (which implies 16-position
           // blocks); other items keep the tile loop compiled without the
           // split's range and merge code.
-          const int lr = item - sm.off[r];
+          const int lr = sorted ? (int)(pf_units[item / per_unit] & 0xffffu) * per_unit + item % per_unit
+                                : item - sm.off[r];
           if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
           else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
           else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
@@ -2370,8 +2255,9 @@ AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
         paged_attention_kernel<true, MODE_DECODE>}},
       {{paged_attention_kernel<false, MODE_MIXED, true>, paged_attention_kernel<false, MODE_PREFILL, true>,
         paged_attention_kernel<false, MODE_DECODE, true>},
-       {paged_attention_kernel<true, MODE_MIXED, true>, paged_attention_kernel<true, MODE_PREFILL, true>,
-        paged_attention_kernel<true, MODE_DECODE, true>}},
+       // E4M3FN launches with prefill rows never carry the KV write
+       // (launch_attention runs the store kernel first).
+       {nullptr, nullptr, paged_attention_kernel<true, MODE_DECODE, true>}},
   };
   return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
 }
@@ -2509,6 +2395,12 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
     }
   }
   const bool store = a->store_slot_mapping != nullptr;
+  // The KV write runs inside the launch except on E4M3FN pools with prefill
+  // rows: there it runs as the store kernel first and the launch reads the
+  // pool (same bytes and outputs; the folded E4M3FN instantiations with
+  // prefill rows spilled registers and measured slower, 108 against 72 us on
+  // 24 decode rows of 256-4096 tokens beside two 512-token chunks).
+  const bool fold = store && !(fp8 && do_pf);
   if (store) {
     if (fp8 && !(a->store_scale_floor > 0.0f))
       return fail(SLO_ERR_INVALID, "paged_attention: the E4M3FN KV write needs store_scale_floor > 0");
@@ -2522,6 +2414,14 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
         (reinterpret_cast<uintptr_t>(a->new_v) % 16))
       return fail(SLO_ERR_INVALID,
                   "paged_attention: new K/V must be contiguous 16-byte aligned bf16 rows, one per query row");
+  }
+  if (store && !fold) {
+    const int rc = slo_store_kvcache(a->new_k, a->new_k_row_stride, a->new_v, a->new_v_row_stride,
+                                     a->store_slot_mapping, a->num_new_rows, a->num_kv_heads, HD, a->kv_dtype,
+                                     const_cast<void*>(a->k_cache), const_cast<void*>(a->v_cache),
+                                     const_cast<float*>(a->k_scale), const_cast<float*>(a->v_scale),
+                                     (int64_t)a->num_blocks * a->block_size, a->store_scale_floor, stream);
+    if (rc) return rc;
   }
   // Workspace: control words, split-K tickets, then decode partials (or, in
   // prefill-only launches, split prefill records).
@@ -2592,12 +2492,12 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   p.counters = reinterpret_cast<int*>(wsb + CTRL_BYTES);
   p.partials = reinterpret_cast<float*>(wsb + PARTIALS_OFFSET);
   p.pf_split_bytes = pf_split_bytes;
-  p.sslots = store ? a->store_slot_mapping : nullptr;
+  p.sslots = fold ? a->store_slot_mapping : nullptr;
   p.nk = static_cast<const uint16_t*>(a->new_k);
   p.nv = static_cast<const uint16_t*>(a->new_v);
   p.nk_stride = a->new_k_row_stride;
   p.nv_stride = a->new_v_row_stride;
-  p.nnew = store ? a->num_new_rows : 0;
+  p.nnew = fold ? a->num_new_rows : 0;
   p.scale_floor = a->store_scale_floor;
   p.num_slots = (int64_t)a->num_blocks * a->block_size;
   // A merge task waits up to 200 ms for its chunks (a whole decode launch
@@ -2624,9 +2524,9 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
   const int mode = do_dec && do_pf ? MODE_MIXED : do_pf ? MODE_PREFILL : MODE_DECODE;
   // With the KV write folded in, the pool's format decides the instantiation
   // (its store quantises); otherwise what the launch reads does.
-  const bool kfp8 = store ? fp8 : fp8_reads;
-  const AttnKernel kernel = attn_kernel(store, kfp8, mode);
-  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[store ? 1 : 0][kfp8 ? 1 : 0][mode];
+  const bool kfp8 = fold ? fp8 : fp8_reads;
+  const AttnKernel kernel = attn_kernel(fold, kfp8, mode);
+  const int64_t slots = (int64_t)ds.cus * ds.wg_per_cu[fold ? 1 : 0][kfp8 ? 1 : 0][mode];
   if (mode == MODE_DECODE) {
     // The shortest chunks whose grid fits what the GPU holds at once; else
     // the longest, when their grid fits DIRECT_MAX_ROUNDS times.
@@ -2639,7 +2539,7 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
       const int64_t dgrid = ((int64_t)p.nd * nch_cap + 7) / 8 * 8 * p.hkv;
       if (dgrid > (steps == max_steps ? DIRECT_MAX_ROUNDS[kfp8 ? 1 : 0] * held : held)) continue;
       void* dargs[] = {&p, const_cast<int*>(&nch_cap), &steps};
-      if (hipLaunchKernel(reinterpret_cast<const void*>(direct_kernel(store, kfp8)), dim3((unsigned)dgrid), dim3(NT),
+      if (hipLaunchKernel(reinterpret_cast<const void*>(direct_kernel(fold, kfp8)), dim3((unsigned)dgrid), dim3(NT),
                           dargs, 0, static_cast<hipStream_t>(stream)) != hipSuccess)
         return fail(SLO_ERR_HIP, "paged_attention: launch failed");
       return check_launch("paged_attention");
