@@ -242,14 +242,19 @@ def test_merge_that_gives_up_is_reported_and_does_not_poison_the_next_launch(dev
     check_workspaces()
     monkeypatch.setenv("SLO_ATTN_MERGE_WAIT_US", "0")
     gave_up = 0
+    nd = len(case.decode_hist)
     for _ in range(3):
-        case.run_gpu(device)
+        out, _ = case.run_gpu(device)
         torch.cuda.synchronize()
         try:
-            gave_up += workspace_events(device)["merges_gave_up"]
+            n = workspace_events(device)["merges_gave_up"]
         except RuntimeError as e:
             assert "gave up waiting" in str(e), e
-            gave_up += int(str(e).split("workspace_check: ")[1].split()[0])
+            n = int(str(e).split("workspace_check: ")[1].split()[0])
+        gave_up += n
+        # a merge that gives up writes NaN to its (row, kv head)'s outputs
+        if n:
+            assert torch.isnan(out[:nd].float()).any(), "a merge gave up but no decode output is NaN"
     print(f"config {index} fp8={kv_fp8}: merges that gave up over 3 launches: {gave_up}")
     if waits:
         assert gave_up > 0, "no merge task gave up: the bounded wait's exit did not run"
