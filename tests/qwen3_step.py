@@ -235,10 +235,12 @@ class Batch:
             return torch.tensor(x, dtype=torch.int32, device=device)
 
         d = self.num_decode
+        pf = m["num_prefill_tokens"] > 0
         meta = MixedAttentionContext(
             d, m["num_prefill_tokens"], i32(m["decode_lens"]) if d else None,
-            i32(m["decode_tables"]) if d else None, i32(m["prefill_cu_q"]), i32(m["prefill_cu_k"]),
-            i32(m["prefill_tables"]), m["max_q"], m["max_k"], m["prefill_has_history"])
+            i32(m["decode_tables"]) if d else None, i32(m["prefill_cu_q"]) if pf else None,
+            i32(m["prefill_cu_k"]) if pf else None, i32(m["prefill_tables"]) if pf else None,
+            m["max_q"], m["max_k"], m["prefill_has_history"])
         return i32(self.slots), meta
 
 
@@ -388,6 +390,19 @@ def run_step(model: Qwen3, batch: Batch, modules, pool: Pool):
     finally:
         reset_context()
     return logits, logits.argmax(dim=-1)
+
+
+def numerics_policy(logits: torch.Tensor, ref_logits: torch.Tensor):
+    """The reference's acceptance rule on each row's fp32 logits (benchmarks/v1/
+    numerics.py:5-18 as check_v1.py:216-236 applies it): top-1 match, relative
+    L2 <= 0.02, cosine >= 0.999, max-abs <= 0.5.  Returns (passing rows, top-1
+    match, rel-L2, cosine, max-abs), one entry per row."""
+    rel = (logits - ref_logits).norm(dim=-1) / ref_logits.norm(dim=-1).clamp_min(1e-12)
+    cos = F.cosine_similarity(logits, ref_logits, dim=-1)
+    max_abs = (logits - ref_logits).abs().amax(dim=-1)
+    top1 = logits.argmax(dim=-1) == ref_logits.argmax(dim=-1)
+    ok = top1 & (rel <= 0.02) & (cos >= 0.999) & (max_abs <= 0.5) & torch.isfinite(rel)
+    return ok, top1, rel, cos, max_abs
 
 
 def top2_gaps(logits: torch.Tensor) -> torch.Tensor:

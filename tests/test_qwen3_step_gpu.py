@@ -33,7 +33,7 @@ import pytest
 import torch
 
 from qwen3_step import (CONDITIONED, Geometry, Pool, Qwen3, Recorder, ReferenceAttention, config4_batch,
-                        quantize_kv, run_step, top2_gaps)
+                        numerics_policy, quantize_kv, run_step, top2_gaps)
 from slo_attn import Attention
 
 pytestmark = pytest.mark.gpu
@@ -82,11 +82,7 @@ def test_qwen3_4b_mixed_step_greedy_and_kv_bytes(device, model, fp8, fused):
     gaps = top2_gaps(ref_logits)
     rows = tokens.numel()
     # the reference's acceptance rule, row by row (numerics.py:5-18, check_v1.py:216-236)
-    rel = (logits - ref_logits).norm(dim=-1) / ref_logits.norm(dim=-1).clamp_min(1e-12)
-    cos = torch.nn.functional.cosine_similarity(logits, ref_logits, dim=-1)
-    max_abs = (logits - ref_logits).abs().amax(dim=-1)
-    top1 = tokens == ref_tokens
-    ok = top1 & (rel <= 0.02) & (cos >= 0.999) & (max_abs <= 0.5) & torch.isfinite(rel)
+    ok, top1, rel, cos, max_abs = numerics_policy(logits, ref_logits)
     print(f"sampled rows {rows}: greedy = reference in {int(top1.sum())}/{rows}, control (fp64) = reference in "
           f"{int((ctl_tokens == ref_tokens).sum())}/{rows}; smallest reference top-2 margin {gaps.min().item():.3f}, "
           f"noise floor tau {tau:.4f}; reference policy passed by {int(ok.sum())}/{rows} rows "
