@@ -38,7 +38,8 @@ device synchronisations.
   fused, Qwen3-4B head 151936 x 2560 bf16) on the step's 26 sampled rows,
   against HBM (the weight read dominates).
 * roofline_decode.read_ceiling: what a plain read of the same byte count
-  achieves on this GPU (slo_attn/read_ceiling, a child process: one-pass
+  achieves on this GPU (read_ceiling, built from read_ceiling.hip next to
+  this file by __graft_entry__.build(), run as a child process: one-pass
   streams into VGPRs and through LDS-DMA, the decode kernels' route), and
   the decode launch's rate as a fraction of the LDS-DMA stream.
 * cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
@@ -57,6 +58,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "slo-aware-llm-serving-engine_amd"))
 sys.path.insert(0, ROOT)
+
+import workloads  # noqa: E402  (seeded synthetic inputs, next to this file)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -87,7 +90,7 @@ class Step:
 
     def __init__(self, w, device, fp8):
         import torch
-        from slo_attn import reserve_workspace, store_kvcache, workloads
+        from slo_attn import reserve_workspace, store_kvcache
         self.w, self.fp8, self.device = w, fp8, device
         dev = workloads.to_device(w, device)
         self.meta, self.slots = dev["meta"], dev["slot_mapping"]
@@ -199,8 +202,8 @@ def hbm(bytes_, us, **extra):
 
 def read_ceiling(nbytes):
     """Achievable read rates for nbytes: the read_ceiling program built next to
-    the library, run as a child process (None when it is not built or fails)."""
-    exe = os.path.join(ROOT, "slo-aware-llm-serving-engine_amd", "slo_attn", "read_ceiling")
+    this file, run as a child process (None when it is not built or fails)."""
+    exe = os.path.join(ROOT, "read_ceiling")
     if not os.path.exists(exe):
         return None
     try:
@@ -225,7 +228,7 @@ def main():
               "(the attention path runs at TP=1 and this build has no multi-GPU path).", file=sys.stderr)
         sys.exit(2)
     import torch
-    from slo_attn import _lib, lm_head_argmax, qk_norm_rope_store, rope_cos_sin, workloads
+    from slo_attn import _lib, lm_head_argmax, qk_norm_rope_store, rope_cos_sin
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -434,7 +437,7 @@ def main():
 def profile(args, device):
     """Eager launches of one kernel kind, for rocprofv3 counter and trace runs."""
     import torch
-    from slo_attn import _lib, lm_head_argmax, qk_norm_rope_store, rope_cos_sin, workloads
+    from slo_attn import _lib, lm_head_argmax, qk_norm_rope_store, rope_cos_sin
     w = workloads.config(args.config)
     st = Step(w, device, fp8=args.kv == "fp8")
     src = torch.empty(256 << 20, dtype=torch.uint8, device=device)
@@ -480,7 +483,7 @@ def cpu_baseline(w):
     import torch
     from oracle import attention as oatt
     from oracle import kvstore
-    from slo_attn.workloads import padded_tables
+    from workloads import padded_tables
 
     meta = {
         "num_decode": w.num_decode, "num_prefill_tokens": sum(w.prefill_q), "decode_lens": w.decode_lens,

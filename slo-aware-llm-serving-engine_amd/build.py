@@ -18,9 +18,6 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "slo_attn")
 LIB = os.path.join(OUT_DIR, "libslo_attn.so")
 SOURCES = ["store_kv.hip", "qk_norm_rope.hip", "lm_head.hip", "metadata.hip", "paged_attention.hip", "capi.cpp"]
-# Stand-alone measurement program (achievable read rates), next to the library.
-CEILING_SRC = "read_ceiling.hip"
-CEILING = os.path.join(OUT_DIR, "read_ceiling")
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
@@ -74,13 +71,6 @@ def build(jobs: int = 4) -> str:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("link failed")
     os.replace(tmp, LIB)
-    tmp = CEILING + ".tmp"
-    res = subprocess.run([hipcc(), *FLAGS, "-x", "hip", os.path.join(CSRC, CEILING_SRC), "-o", tmp],
-                         capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed on {CEILING_SRC}")
-    os.replace(tmp, CEILING)
     return LIB
 
 

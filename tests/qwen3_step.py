@@ -249,7 +249,7 @@ def config4_batch(vocab: int, seed: int = 4, num_blocks: int = 681, block_size: 
     """64 decode rows with end_pos uniform in [512, 4096] and one 1024-token chunk.
 
     Lengths and block tables are drawn exactly as the single-layer workload of
-    the same step (slo_attn.workloads.config(4)); token ids come after.
+    the same step (workloads.config(4)); token ids come after.
     """
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(512, 4097, (num_decode,), generator=g).tolist()

@@ -110,7 +110,7 @@ def test_direct_decode_chunk_lengths(device, kv_fp8, nd, cap, hq, hkv):
 
 # --------------------------------------------- benchmark configurations
 def _workload_case(index, kv_fp8=False, hq=32, hkv=8):
-    from slo_attn import workloads
+    import workloads
     w = workloads.config(index, hq, hkv)
     nd = w.num_decode
     case = Case([L - 1 for L in w.decode_lens], w.prefill_prefix, w.prefill_q, hq=hq, hkv=hkv, seed=1000 + index,

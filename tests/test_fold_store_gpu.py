@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from slo_attn import (Attention, MixedAttentionContext, forward_mixed, reserve_workspace, reset_context,
-                      set_context, store_kvcache, workloads)
+                      set_context, store_kvcache)
+import workloads
 from slo_attn.ops import paged_attention
 from types import SimpleNamespace
 

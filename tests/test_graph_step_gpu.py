@@ -81,6 +81,23 @@ def test_metadata_kernel_matches_oracle(device, seed):
         assert want["cu_seqlens_q"][:len(rows) + 1] == m["prefill_cu_q"]
 
 
+def test_metadata_kernel_flat_offsets_kat(device):
+    # tests/test_v1_state.py:88-101 through the metadata kernel: one decode row
+    # at position 256 and the first 256-token chunk of a 513-token prompt.
+    bs = 256
+    tables = [[0, 1], [2, 3, 4]]
+    buf = MixedStepBuffers(1, 1, 257, 3, bs, 3 * bs, device)
+    buf.load([256], [(0, 256)], tables, list(range(257)))
+    buf.build()
+    torch.cuda.synchronize()
+    pos = buf.positions.cpu().tolist()
+    assert tuple(pos[:3]) == (256, 0, 1)
+    cu = buf.cu_q.cpu().tolist()
+    assert (0, 1) + tuple(1 + c for c in cu[1:]) == (0, 1, 257)
+    assert buf.slot_mapping.cpu().tolist() == [256] + metadata.expected_slots(tables[1], 0, 256, bs)
+    assert buf.decode_lens.cpu().tolist() == [257]
+
+
 @pytest.mark.parametrize("kv", ["bf16", "fp8_e4m3fn"])
 def test_graph_replays_equal_eager(device, kv):
     geom = Geometry(num_layers=2, hidden=256, num_heads=8, num_kv_heads=2, intermediate=512, vocab=1000,

@@ -208,6 +208,31 @@ def test_gather_pages_and_slots_kats():
         oatt.gather_pages(cache, [0], 3)
 
 
+def _flat_offsets(meta):
+    """Flat query offsets of a mixed step: each decode row one token, then the
+    prefill rows (BatchMetadata.query_offsets, batch_metadata.py:94-118)."""
+    d = meta["num_decode"]
+    return tuple(range(d + 1)) + tuple(d + c for c in meta["prefill_cu_q"][1:])
+
+
+def test_flat_offsets_kat():
+    # tests/test_v1_state.py:88-101: a 256-token sequence decodes its token at
+    # position 256 beside the first 256-token chunk of a 513-token prompt, one
+    # step, 256-token blocks: query_offsets (0, 1, 257), positions[:3]
+    # (256, 0, 1).
+    bs = 256
+    tables = [[0, 1], [2, 3, 4]]
+    meta = metadata.mixed_metadata([257], tables[:1], [0], [256], tables[1:])
+    assert _flat_offsets(meta) == (0, 1, 257)
+    step = metadata.padded_step([256, 0], [1, 256], 1, 1, 257, tables, bs)
+    assert tuple(step["positions"][:3]) == (256, 0, 1)
+    assert step["positions"] == [256] + list(range(256))
+    assert step["slot_mapping"][0] == metadata.slot_of(tables[0], 256, bs) == 256
+    assert step["slot_mapping"][1:] == metadata.expected_slots(tables[1], 0, 256, bs)
+    assert step["decode_lens"] == [257] and step["cu_seqlens_q"] == [0, 256] and step["cu_seqlens_k"] == [0, 256]
+    assert not meta["prefill_has_history"]  # the chunk starts at position 0
+
+
 def test_mixed_oracle_equals_dense_on_concatenated_history():
     # Mirrors tests/test_v1_reference_gpu.py:10-45 on the CPU: decode 256+1,
     # prefill 249+8 across a page boundary, and a cold 17-token prefill.

@@ -13,7 +13,8 @@ import ctypes
 import pytest
 import torch
 
-from slo_attn import _lib, workloads
+import workloads
+from slo_attn import _lib
 from slo_attn.ops import _stream, paged_attention
 
 pytestmark = pytest.mark.gpu
