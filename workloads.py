@@ -152,7 +152,7 @@ def config(index: int, hq: int = HQ, hkv: int = HKV) -> Workload:
 
 def to_device(w: Workload, device, kv_fp8: bool = False):
     """Device tensors + MixedAttentionContext for ``w`` (prepare_mixed layout)."""
-    from .mixed_attention import MixedAttentionContext
+    from slo_attn import MixedAttentionContext
 
     def i32(x):
         return torch.tensor(x, dtype=torch.int32, device=device)
