@@ -21,9 +21,10 @@ device synchronisations.
 * value: whole-step throughput in tokens/s (1048 tokens per step) over the
   --steps timed steps; ms_per_step is the same measurement.
 * roofline: the step's attention launch (bf16 pool, KV write folded in)
-  against HBM bandwidth: achieved = algorithmic bytes per launch (decode KV
-  bytes + prefill K/V + q + out + the folded write's new rows read and slots
-  written) / its per-launch time.  roofline_decode / roofline_prefill time the
+  against HBM bandwidth: achieved = algorithmic bytes per launch (cached K/V
+  read: decode contexts and prefill prefixes; each new token's bf16 K/V row
+  read once and its pool slot written once; q read and out written) / its
+  per-launch time.  roofline_decode / roofline_prefill time the
   split launches (decode rows only against HBM, prefill rows only against bf16
   MFMA peak), the mode that mirrors the reference's per-phase flash-attn calls;
   roofline_prefill carries the MFMA-busy fraction that rocprofv3 counters gave
@@ -150,14 +151,20 @@ class Step:
         return self.w.decode_kv_bytes(self.elem(), self.scale_bytes())
 
     def step_bytes(self, fold):
-        """Algorithmic bytes of one mixed launch: decode KV + prefill K/V + q and out,
-        plus, with the KV write folded in, the new rows read and the slots written."""
+        """Algorithmic bytes of one mixed launch: q read and out written, plus the
+        pool K/V read (decode contexts, prefill prefixes and new rows).  With the KV
+        write folded in, each new token's K/V counts once as read (its bf16 row of
+        new_k/new_v) and once as written (its pool slot); the kernel's reads of it
+        back from the pool add nothing."""
         w = self.w
-        pre_tokens = sum(n + p for n, p in zip(w.prefill_q, w.prefill_prefix))
-        pre = pre_tokens * self.hkv * (2 * self.d * self.elem() + 2 * self.scale_bytes())
+        row = self.hkv * (2 * self.d * self.elem() + 2 * self.scale_bytes())
         qo = 2 * w.num_tokens * self.hq * self.d * 2
-        store = 2 * w.num_tokens * self.hkv * self.d * 2 * 2 if fold else 0
-        return self.decode_bytes() + pre + qo + store
+        if not fold:
+            pre_tokens = sum(n + p for n, p in zip(w.prefill_q, w.prefill_prefix))
+            return self.decode_bytes() + pre_tokens * row + qo
+        cached = self.decode_bytes() - w.num_decode * row + sum(w.prefill_prefix) * row
+        new = w.num_tokens * (2 * self.hkv * self.d * 2 + row)
+        return cached + new + qo
 
 
 def graph_time(fn, n_per_graph=NSETS, target=LAUNCH_TARGET, replays=None):
@@ -213,12 +220,36 @@ def read_ceiling(nbytes):
         return None
 
 
+def sources_sha16():
+    """sha256 (first 16 hex digits) of the HIP sources the library is built from,
+    in name order: profiles record the value of the build they measured."""
+    import hashlib
+    csrc = os.path.join(ROOT, "slo-aware-llm-serving-engine_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def load_profile_json(name):
     path = os.path.join(ROOT, "profiles", name)
     if os.path.exists(path):
         with open(path) as fh:
             return json.load(fh)
     return {}
+
+
+def profile_stamp(profile, name):
+    """Which build a profile-sourced field comes from: the sources hash the profile
+    recorded and whether it equals the current sources' (a field from another
+    build is kept but marked)."""
+    recorded = profile.get("meta", {}).get("sources_sha16")
+    current = sources_sha16()
+    return {"file": f"profiles/{name}", "sources_sha16": recorded, "current_sources_sha16": current,
+            "matches_build": recorded == current}
 
 
 def main():
@@ -347,7 +378,7 @@ def main():
     counters = all_counters.get("prefill_3", {})
 
     def traffic_of(kernel):
-        return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic else None
+        return round(traffic[kernel]["traffic_mb"] * 1e6) if kernel in traffic and kernel != "meta" else None
 
     # ---- 16 short decode rows (64-1024 tokens): a pure decode step (forward_mixed,
     # KV write folded in) and the decode launch alone, both pool formats
@@ -430,6 +461,12 @@ def main():
                                        rows=sample_rows, vocab=vocab, hidden=hidden,
                                        torch_linear_argmax_us=round(t_lm_torch, 2)),
         "cpu_baseline": cpu,
+        # traffic and mfma_busy values above are read from these committed
+        # rocprofv3 summaries, not measured in this run
+        "profile_fields_from": {
+            "traffic": profile_stamp(traffic, "traffic_mixed_24decode_2x512chunk.json"),
+            "mfma_busy": profile_stamp(all_counters, "counters_paged_attention.json"),
+        },
     }
     print(json.dumps(line))
 
