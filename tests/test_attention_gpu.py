@@ -132,10 +132,11 @@ def test_benchmark_config_bf16(device, index):
     print(f"config {index}: max-abs {mx:.3e} mean-abs {mn:.3e}")
 
 
-@pytest.mark.parametrize("index", [0, 1, 2, 3])
+@pytest.mark.parametrize("index", [0, 1, 2, 3, 4])
 def test_benchmark_config_fp8(device, index):
     # config 1 (cold prefill rows only) reads nothing from the E4M3FN pool and
-    # runs the bf16 kernel; configs 2 and 3 read prefixes from it
+    # runs the bf16 kernel; configs 2 and 3 read prefixes from it; config 4 is
+    # one model layer's step (64 decode rows beside a 1,024-token chunk)
     case = _workload_case(index, kv_fp8=True)
     (mx, mn), _, _ = _check(case, device)
     print(f"config {index} fp8: max-abs {mx:.3e} mean-abs {mn:.3e}")
@@ -207,15 +208,27 @@ def test_prefill_rows_split_in_key_halves(device, kv_fp8, phases):
             assert torch.equal(again.view(torch.int16), got.view(torch.int16))
 
 
-def test_split_phases_match_fused(device):
-    case = Case([300, 1000, 17], [512], [200], seed=9)
+@pytest.mark.parametrize("kv_fp8", [False, True])
+def test_split_phases_match_fused(device, kv_fp8):
+    # Each phase alone against the mixed launch: both pass the gate against
+    # the oracle and agree to the gate's bounds; with a bf16 pool the decode
+    # phase (the direct kernel, chunks of the mixed launch's length here) and
+    # the prefill phase (the same prefill items) are bit-equal to it.
+    case = Case([300, 1000, 17], [512], [200], seed=9, kv_fp8=kv_fp8)
     fused, _ = case.run_gpu(device, phases=3)
     dec, _ = case.run_gpu(device, phases=1)
     pre, _ = case.run_gpu(device, phases=2)
     torch.cuda.synchronize()
+    want, _ = case.oracle()
     d = 3
-    assert torch.equal(fused[:d], dec[:d])
-    assert torch.equal(fused[d:], pre[d:])
+    for got in (dec[:d], fused[:d]):
+        assert_close_gate(got, want[:d])
+    assert_close_gate(dec[:d], fused[:d])
+    for got in (pre[d:], fused[d:]):
+        assert_close_gate(got, want[d:])
+    if not kv_fp8:
+        assert torch.equal(fused[:d], dec[:d])
+        assert torch.equal(fused[d:], pre[d:])
 
 
 def test_deterministic_across_launches(device):
