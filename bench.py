@@ -79,6 +79,9 @@ def parse():
     ap.add_argument("--kv", choices=["bf16", "fp8"], default="bf16", help="pool format of --profile runs")
     ap.add_argument("--events", type=int, default=100, help="launches of --profile runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the step line: one JSON line per workload config 0-4 (step, decode and "
+                         "prefill launches on both pool formats, and the CPU oracle's step time)")
     ap.add_argument("--profile", choices=["fused", "decode", "prefill", "qk", "lm_head"], default=None,
                     help="only launch this attention phase or kernel (eagerly, for rocprofv3 counter runs) on "
                          "--config / --kv, plus one 256 MiB device copy whose counters calibrate "
@@ -265,6 +268,8 @@ def main():
     torch.cuda.set_device(device)
     if args.profile:
         return profile(args, device)
+    if args.configs:
+        return config_table(args, device)
 
     w = workloads.config(3)
     st = Step(w, device, fp8=False)
@@ -515,7 +520,45 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(w):
+def config_table(args, device):
+    """Every workload config: graph-replayed step (forward_mixed, KV write included), decode-only
+    and prefill-only launches on bf16 and E4M3FN pools, with the algorithmic rates, and the CPU
+    oracle's time for the same step (bf16 pool) unless --no-cpu-baseline."""
+    import torch
+    from slo_attn import _lib
+    for idx in range(5):
+        w = workloads.config(idx)
+        line = {"config": idx, "workload": w.name, "new_tokens": w.num_tokens, "decode_rows": w.num_decode,
+                "decode_context_sum": sum(w.decode_lens), "prefill_chunks": list(w.prefill_q),
+                "prefill_prefixes": list(w.prefill_prefix), "prefill_gflop": round(w.prefill_flops() / 1e9, 3)}
+        for fp8 in (False, True):
+            st = Step(w, device, fp8=fp8)
+            r = {}
+            t, _ = graph_time(st.step)
+            r["step_us"] = round(t, 2)
+            r["step_tokens_per_s"] = round(w.num_tokens / (t * 1e-6), 1)
+            if w.num_decode:
+                t, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_DECODE))
+                r["decode_us"] = round(t, 2)
+                r["decode_kv_bytes"] = st.decode_bytes()
+                r["decode_GBps"] = round(st.decode_bytes() / (t * 1e-6) / 1e9, 1)
+                r["decode_frac_hbm"] = round(st.decode_bytes() / (t * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            if w.prefill_q:
+                t, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_PREFILL))
+                r["prefill_us"] = round(t, 2)
+                r["prefill_TFLOPs"] = round(w.prefill_flops() / (t * 1e-6) / 1e12, 1)
+                r["prefill_frac_mfma"] = round(w.prefill_flops() / (t * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
+            if w.num_decode and w.prefill_q:
+                r["split_us"] = round(r["decode_us"] + r["prefill_us"], 2)
+            line["e4m3fn" if fp8 else "bf16"] = r
+            del st
+            torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            line["cpu_oracle"] = cpu_baseline(w, runs=3)
+        print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(w, runs=5):
     """The CPU oracle (fp32 torch on the host cores) on the same step: store, then attention."""
     import torch
     from oracle import attention as oatt
@@ -524,8 +567,9 @@ def cpu_baseline(w):
 
     meta = {
         "num_decode": w.num_decode, "num_prefill_tokens": sum(w.prefill_q), "decode_lens": w.decode_lens,
-        "decode_tables": padded_tables(w.decode_tables), "prefill_cu_q": w.cu_q, "prefill_cu_k": w.cu_k,
-        "prefill_tables": padded_tables(w.prefill_tables), "prefill_has_history": w.has_history,
+        "decode_tables": padded_tables(w.decode_tables) if w.decode_tables else [], "prefill_cu_q": w.cu_q,
+        "prefill_cu_k": w.cu_k, "prefill_tables": padded_tables(w.prefill_tables) if w.prefill_tables else [],
+        "prefill_has_history": w.has_history,
     }
     torch.set_num_threads(os.cpu_count() or 1)
     kc = w.k_cache.clone()
@@ -538,14 +582,14 @@ def cpu_baseline(w):
 
     run()
     times = []
-    for _ in range(5):
+    for _ in range(runs):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {"value": round(w.num_tokens / t, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "cpu": cpu_model(), "kind": "port",
-            "sample": f"full step ({w.num_tokens} tokens, bf16 pool): median of 5 after 1 warm-up, "
+            "cpu": cpu_model(), "kind": "port", "ms_per_step": round(t * 1e3, 1),
+            "sample": f"full step ({w.num_tokens} tokens, bf16 pool): median of {runs} after 1 warm-up, "
                       f"{t * 1e3:.1f} ms per step"}
 
 
