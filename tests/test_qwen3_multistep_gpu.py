@@ -1,8 +1,10 @@
 """Consecutive Qwen3-4B mixed steps through the captured step graph, tokens fed back.
 
-Step 0 holds 16 decode rows (end_pos uniform in [512, 2048], seed 7) and one
-cold 256-token prefill chunk; in steps 1-3 every row, the chunk's included,
-decodes its next token.  So from step 1 on, each decode row reads as history
+Step 0 holds D decode rows (end positions uniform in [512, hi], seed 7) and
+one cold C-token prefill chunk; in steps 1-3 every row, the chunk's included,
+decodes its next token.  Two sizes, each on bf16 and E4M3FN pools: D = 16,
+C = 256, hi = 2048, and the config-4 size (64 decode rows, end positions in
+[512, 4096], a 1,024-token chunk).  So from step 1 on, each decode row reads as history
 the K/V that the earlier steps of the same path wrote into the pool, and the
 chunk's row reads the 256 keys that its prefill wrote.
 
@@ -30,7 +32,7 @@ from slo_attn import Attention, MixedStepBuffers, MixedStepGraph
 
 pytestmark = pytest.mark.gpu
 
-D, C, STEPS, BS = 16, 256, 4, 256
+STEPS, BS = 4, 256
 
 
 @pytest.fixture(scope="module")
@@ -41,9 +43,9 @@ def model(device):
     torch.cuda.empty_cache()
 
 
-def _plan(vocab: int):
+def _plan(vocab: int, D: int, C: int, hi: int):
     g = torch.Generator().manual_seed(7)
-    lens0 = torch.randint(512, 2049, (D,), generator=g).tolist()
+    lens0 = torch.randint(512, hi + 1, (D,), generator=g).tolist()
     first = [L - 1 for L in lens0] + [None]          # decode rows' step-0 positions; the chunk row
     need = [L - 1 + STEPS for L in lens0] + [C + STEPS]
     pages = [(n + BS - 1) // BS for n in need]
@@ -57,11 +59,13 @@ def _plan(vocab: int):
     return first, tables, ids0, num_blocks
 
 
-@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "e4m3fn"])
-def test_multistep_graph_matches_reference(device, model, fp8):
+@pytest.mark.parametrize("fp8,D,C,hi", [(False, 16, 256, 2048), (True, 16, 256, 2048), (False, 64, 1024, 4096),
+                                        (True, 64, 1024, 4096)],
+                         ids=["bf16", "e4m3fn", "bf16-config4-size", "e4m3fn-config4-size"])
+def test_multistep_graph_matches_reference(device, model, fp8, D, C, hi):
     geom = model.geom
     hq, hkv, d, layers = geom.num_heads, geom.num_kv_heads, geom.head_dim, geom.num_layers
-    first, tables, ids0, num_blocks = _plan(geom.vocab)
+    first, tables, ids0, num_blocks = _plan(geom.vocab, D, C, hi)
     pool = Pool(geom, num_blocks, BS, device, fp8)
     ref_pool = pool.clone()
     width = max(len(t) for t in tables)
