@@ -277,7 +277,10 @@ __device__ __forceinline__ void softmax_half(f32x4 (&sh)[2][NQT], float (&m)[NQT
       for (int i = 0; i < 4; ++i) {
         const float e = __builtin_amdgcn_exp2f(fmaf(sh[mm][nt][i], c, -cm));
         rs += e;
-        sh[mm][nt][i] = SCALED ? e * vsc[i] : e;
+        // (Boundary tiles: the V scales of keys past the valid ones are
+        // whatever LDS holds there.)
+        const float v = MASK && SCALED ? (kh + 16 * mm + 4 * g + i < ntok ? vsc[i] : 0.0f) : vsc[i];
+        sh[mm][nt][i] = SCALED ? e * v : e;
       }
     }
     rs = col_sum(rs);
@@ -1464,10 +1467,10 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // wavefront lands at byte 16*i of a 1 KiB stripe of 4 rows), so the next
   // tile is in flight while the current one is consumed.  E4M3FN pool bytes
   // take the same route into the second half of the next tile's buffer (K
-  // codes, then V codes, 8 KiB each, unswizzled) and their scales straight to
-  // sm.u.pf.ks/vs; after the current tile's compute the workgroup decodes
-  // them into that buffer's bf16 K and V tiles (commit_tile).  Rows past the
-  // valid keys are zero.
+  // codes, then V codes, 8 KiB each, 16-byte chunk c of row r in slot
+  // c ^ (r & 7)) and their scales straight to sm.u.pf.ks/vs; the MFMA
+  // operands are converted from the codes where they are read.  Rows past the
+  // valid keys are zero (bf16) or masked where read (codes).
   const int* prow = p.ptab + (int64_t)r * p.ptab_stride;
   const int npages = paged ? (kend + p.block_size - 1) / p.block_size : 0;
   const bool cached = npages <= MAX_PAGES;
@@ -1529,23 +1532,36 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     if (fresh) ok = true;
     const int nv = ok ? ntok : 0;
     if (src_fp8 && !fresh) {
-      // All 64 rows of the tile's block are loaded (they lie in that block,
-      // block_size being a multiple of 64; without a valid block, rows of
-      // block 0 stand in): rows from nv on are zeroed when committed.
-      const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + (ok ? kbase : 0);
-      const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + (ok ? vbase : 0);
+      // The codes stay codes: K and V code rows (128 bytes, 16-byte chunk c
+      // of row r at slot c ^ (r & 7)) go to the second half of the buffer and
+      // the MFMA operands are converted from them as they are read.  All 64
+      // rows of the tile's block are loaded (they lie in that block,
+      // block_size being a multiple of 64); rows past the valid keys are
+      // masked where they are read.  Without a valid block the codes and
+      // scales are zeros (keys of score 0 and value 0).
       uint8_t* stg = (buf ? st1 : st0) + TILE_BYTES;
+      if (!ok) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) st16(stg + 16 * (it * NT + tid), u32x4{0, 0, 0, 0});
+        if (tid < TT) {
+          sm.u.pf.ks[buf][tid] = 0.0f;
+          sm.u.pf.vs[buf][tid] = 0.0f;
+        }
+        return nv;
+      }
+      const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + kbase;
+      const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + vbase;
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
-        const int q = it * NT + tid;  // 16-byte piece q: row q >> 3, bytes 16 * (q & 7)
-        const int off = (q >> 3) * krow + 16 * (q & 7);
+        const int q = it * NT + tid;  // 16-byte slot q: row q >> 3, slot q & 7
+        const int off = (q >> 3) * krow + 16 * ((q & 7) ^ ((q >> 3) & 7));
         const uint32_t dst = lds_addr(stg + 16 * (it * NT + wave * 64));
         dma16(kc + off, dst);
         dma16(vc + off, dst + 8192);
       }
       if (wave < 2) {
         const float* sc = wave ? p.v_scale : p.k_scale;
-        dma4(sc + (ok ? (slot0 + lane) * p.hkv + h : 0), lds_addr(wave ? sm.u.pf.vs[buf] : sm.u.pf.ks[buf]));
+        dma4(sc + (slot0 + lane) * p.hkv + h, lds_addr(wave ? sm.u.pf.vs[buf] : sm.u.pf.ks[buf]));
       }
       return nv;
     }
@@ -1597,11 +1613,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     }
     return ret;
   };
-  // E4M3FN tiles only: once the codes and scales issued for buffer `buf` have
-  // landed, every thread decodes its 4 rows' K and V chunks (the swizzled bf16
-  // layout of the DMA path) into that buffer; the V tile overwrites the codes,
-  // so all of them are read before any is written.  Rows from nv on become
-  // zeros and their scales 0.
+  // After the tile of buffer `buf` is issued: tiles of bf16 rows in an
+  // E4M3FN launch take unit scales; tiles of E4M3FN codes need nothing (their
+  // operands are converted where they are read).
   auto commit_tile = [&](int buf, int nv, int kv0) {
     if (!src_fp8) {
       // bf16 rows of an E4M3FN launch: unit scales (read after the next
@@ -1612,29 +1626,6 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
       }
       return;
     }
-    uint8_t* tb = buf ? st1 : st0;
-    const uint8_t* stg = tb + TILE_BYTES;
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    __syncthreads();
-    u32x2 kx[4], vx[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      const bool okr = row < nv;
-      kx[it] = okr ? ld8(stg + row * HD + 8 * ((tid & 15) ^ (row & 15))) : u32x2{0, 0};
-      vx[it] = okr ? ld8(stg + 8192 + row * HD + 8 * ((tid & 15) ^ ((row & 7) << 1))) : u32x2{0, 0};
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      st16(tb + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(kx[it]));
-      st16(tb + TILE_BYTES + row * ROWB + ((tid & 15) << 4), fp8x8_to_bf16x8(vx[it]));
-    }
-    if (tid < TT && tid >= nv) {
-      sm.u.pf.ks[buf][tid] = 0.0f;
-      sm.u.pf.vs[buf][tid] = 0.0f;
-    }
   };
 
   // Lane-constant LDS byte offsets of the MFMA operands within a tile: K rows
@@ -1642,6 +1633,18 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   int koff[4], voff[8];
 #pragma unroll
   for (int st = 0; st < 4; ++st) koff[st] = k_off(n, 4 * st + g);
+  // Code tiles (E4M3FN): K code row r at 128 r with 16-byte chunk c in slot
+  // c ^ (r & 7) (K fragment reads: row n of each 16-row block, chunk
+  // 2 (jj >> 1) + g / 2, bytes 8 (g & 1)); the V^T reads pass row j = n / 2
+  // of an 8-row block (key 4g + j, or 16 + 4g + j - 4), bytes 8 (n & 1).
+  int kcoff[4] = {0, 0, 0, 0}, vcoff = 0, vcsw = 0;
+  if constexpr (FP8) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) kcoff[st] = n * 128 + 16 * ((2 * st + (g >> 1)) ^ (n & 7)) + 8 * (g & 1);
+    const int vkey = (n >> 1) < 4 ? 4 * g + (n >> 1) : 12 + 4 * g + (n >> 1);
+    vcoff = vkey * 128 + 8 * (n & 1);
+    vcsw = vkey & 7;
+  }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) voff[dt] = v_off(4 * g + (n >> 2), 2 * dt + ((n & 3) >> 1)) + ((n & 1) << 3);
 
@@ -1684,8 +1687,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // The rescale of O (rare with the lazy offset) sits between the regions.
   // Interior tiles (no key past the valid rows or the causal edge) run in a
   // loop of their own without masking code.
-  auto tile = [&](auto mask_tag, int kv0, int j) {
+  auto tile = [&](auto mask_tag, auto codes_tag, int kv0, int j) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr bool CODES = decltype(codes_tag)::value;  // E4M3FN codes in the buffer's second half
     const int buf = j & 1;
     const int ntok = min(TT, kend - kv0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -1693,11 +1697,40 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     const bool more = kv0 + TT < kstop;
     const uint8_t* kt = buf ? st1 : st0;
     const uint8_t* vt = kt + TILE_BYTES;
-    // K fragment jj of half h: rows 16*(2h + (jj & 1)) + n, k-step jj >> 1.
-    auto kread_h = [&](int h, int jj) { return ld16(kt + (2 * h + (jj & 1)) * 16 * ROWB + koff[jj >> 1]); };
-    auto vread = [&](int i) {  // V^T operand: k-step (half) i >> 3, d-tile i & 7
-      const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
-      return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
+    // Boundary tiles of codes: byte j of a V^T read is key kperm(j) of the
+    // half (keys 4g + j, then 16 + 4g + j - 4); kept when below ntok.
+    uint64_t keep0 = ~0ull, keep1 = ~0ull;
+    if constexpr (CODES && MASK) {
+      keep0 = keep1 = 0;
+#pragma unroll
+      for (int jb = 0; jb < 8; ++jb) {
+        const int key = (jb < 4 ? 4 * g + jb : 12 + 4 * g + jb);
+        keep0 |= (key < ntok ? 0xffull : 0ull) << (8 * jb);
+        keep1 |= (32 + key < ntok ? 0xffull : 0ull) << (8 * jb);
+      }
+    }
+    // K fragment jj of half h: rows 16*(2h + (jj & 1)) + n, k-step jj >> 1
+    // (from codes: the 8 bytes of d = 32 (jj >> 1) + 8g.. of that row).
+    auto kread_h = [&](int h, int jj) -> u32x4 {
+      if constexpr (CODES) return fp8x8_to_bf16x8(ld8(vt + (2 * h + (jj & 1)) * 16 * 128 + kcoff[jj >> 1]));
+      else return ld16(kt + (2 * h + (jj & 1)) * 16 * ROWB + koff[jj >> 1]);
+    };
+    auto vread = [&](int i) -> bf16x8 {  // V^T operand: k-step (half) i >> 3, d-tile i & 7
+      if constexpr (CODES) {
+        // Transposed byte read of the 8 keys of this lane's operand slots
+        // (d = 16 (i & 7) + n); codes of keys past the valid ones (NaN
+        // patterns possible) are zeroed in boundary tiles.
+        u32x2 c = lds_tr8(vt + 8192 + (i >> 3) * 32 * 128 + vcoff + 16 * ((i & 7) ^ vcsw));
+        if constexpr (MASK) {
+          const uint64_t keep = (i >> 3) ? keep1 : keep0;
+          c.x &= (uint32_t)keep;
+          c.y &= (uint32_t)(keep >> 32);
+        }
+        return as_bf16x8(fp8x8_to_bf16x8(c));
+      } else {
+        const uint8_t* va0 = vt + (i >> 3) * 32 * ROWB + voff[i & 7];
+        return join_tr(lds_tr16(va0), lds_tr16(va0 + 16 * ROWB));
+      }
     };
     u32x4 kf[8];
     if (active) {
@@ -1769,12 +1802,29 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   // its MFMA operand reads take lane offsets plus immediates (three 512-token
   // chunks after prefixes 0/2048/512, prefill-only: about 71 -> 68 us; 24
   // decode rows of 256-4096 tokens and two 512-token chunks: 68.2 -> 67.5 us).
-  for (; kv0 + TT < kstop && tfirst + j + 1 < n_int; kv0 += 2 * TT, j += 2) {
-    tile(std::integral_constant<bool, false>(), kv0, 0);
-    tile(std::integral_constant<bool, false>(), kv0 + TT, 1);
+  using F = std::integral_constant<bool, false>;
+  using T = std::integral_constant<bool, true>;
+  auto tiles = [&](auto codes_tag) {
+    for (; kv0 + TT < kstop && tfirst + j + 1 < n_int; kv0 += 2 * TT, j += 2) {
+      tile(F(), codes_tag, kv0, 0);
+      tile(F(), codes_tag, kv0 + TT, 1);
+    }
+    for (; kv0 < kstop && tfirst + j < n_int; kv0 += TT, ++j) tile(F(), codes_tag, kv0, j);
+    for (; kv0 < kstop; kv0 += TT, ++j) tile(T(), codes_tag, kv0, j);
+  };
+  // E4M3FN launches read every tile of a paged row as codes (the store of the
+  // step's new tokens ran before the launch).
+  if constexpr (FP8) {
+    if (src_fp8) tiles(T());
+    else tiles(F());
+  } else {
+    for (; kv0 + TT < kstop && tfirst + j + 1 < n_int; kv0 += 2 * TT, j += 2) {
+      tile(F(), F(), kv0, 0);
+      tile(F(), F(), kv0 + TT, 1);
+    }
+    for (; kv0 < kstop && tfirst + j < n_int; kv0 += TT, ++j) tile(F(), F(), kv0, j);
+    for (; kv0 < kstop; kv0 += TT, ++j) tile(T(), F(), kv0, j);
   }
-  for (; kv0 < kstop && tfirst + j < n_int; kv0 += TT, ++j) tile(std::integral_constant<bool, false>(), kv0, j);
-  for (; kv0 < kstop; kv0 += TT, ++j) tile(std::integral_constant<bool, true>(), kv0, j);
 
   if constexpr (SPLITK) {
     if (two) {
