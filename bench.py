@@ -50,6 +50,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import subprocess
@@ -65,7 +66,8 @@ import workloads  # noqa: E402  (seeded synthetic inputs, next to this file)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "mixed-step attn tokens/s; decode KV HBM GB/s (% of peak); prefill MFMA util"
-NSETS = 4            # pool copies rotated by consecutive launches
+NSETS = 4            # pool copies rotated by consecutive launches (at least)
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache: rotated copies read at least twice this
 SETTLE_S = 0.3       # untimed replays before each timed measurement
 LAUNCH_TARGET = 1200  # launches per per-launch measurement
 
@@ -90,7 +92,7 @@ def parse():
 
 
 class Step:
-    """One attention workload on the GPU with NSETS pool copies (bf16, or E4M3FN)."""
+    """One attention workload on the GPU with `nsets` pool copies (bf16, or E4M3FN)."""
 
     def __init__(self, w, device, fp8):
         import torch
@@ -101,8 +103,15 @@ class Step:
         self.q, self.k, self.v = dev["q"], dev["k"], dev["v"]
         self.hq, self.hkv, self.d = w.q.shape[1], w.k.shape[1], w.q.shape[2]
         base_k, base_v = w.k_cache.to(device), w.v_cache.to(device)
+        # Enough pool copies that the bytes the launches read from them between
+        # two visits of one copy exceed twice the Infinity Cache, so every
+        # launch reads its KV from HBM (4 at least; 4 when nothing is read
+        # from the pool).
+        row = self.hkv * (2 * self.d * self.elem() + 2 * self.scale_bytes())
+        read = self.decode_bytes() + sum(w.prefill_prefix) * row
+        self.nsets = NSETS if read == 0 else int(min(32, max(NSETS, math.ceil(2 * MALL_BYTES / read))))
         self.pools = []
-        for _ in range(NSETS):
+        for _ in range(self.nsets):
             if fp8:
                 nblk, bs, hkv, d = base_k.shape
                 kc = torch.empty(nblk, bs, hkv, d, dtype=torch.uint8, device=device)
@@ -125,14 +134,14 @@ class Step:
     def step(self, i):
         """forward_mixed as the engine calls it (KV write folded in on a bf16 pool)."""
         from slo_attn import _lib, forward_mixed, store_kvcache
-        kc, vc, ks, vs = self.pools[i % NSETS]
+        kc, vc, ks, vs = self.pools[i % self.nsets]
         return forward_mixed(self.q, self.k, self.v, kc, vc, self.ctx, self.w.scale, store_kvcache, ks, vs,
                              phases=_lib.PHASE_ALL)
 
     def attn(self, i, phases, fold=False):
         """One attention launch without the KV write (or with it folded in)."""
         from slo_attn.ops import paged_attention
-        kc, vc, ks, vs = self.pools[i % NSETS]
+        kc, vc, ks, vs = self.pools[i % self.nsets]
         meta, w = self.meta, self.w
         store = dict(store_slot_mapping=self.slots, new_k=self.k, new_v=self.v) if fold else {}
         history = w.has_history or fold
@@ -143,6 +152,10 @@ class Step:
             prefill_cu_q=meta.prefill_cu_q, prefill_cu_k=meta.prefill_cu_k, max_q=meta.max_q, max_k=meta.max_k,
             prefill_tables=meta.prefill_tables if history else None, k=None if history else self.k[w.num_decode:],
             v=None if history else self.v[w.num_decode:], phases=phases, out=self.out, **store)
+
+    def time(self, fn):
+        """graph_time over one launch per pool copy."""
+        return graph_time(fn, n_per_graph=self.nsets)
 
     def elem(self):
         return 1.0 if self.fp8 else 2.0
@@ -276,22 +289,22 @@ def main():
     hq, hkv, d = st.hq, st.hkv, st.d
     tokens = w.num_tokens
 
-    # ---- whole-step throughput: graph replays of NSETS consecutive steps
-    for i in range(max(args.warmup, NSETS)):
+    # ---- whole-step throughput: graph replays of one step per pool copy
+    for i in range(max(args.warmup, st.nsets)):
         st.step(i)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for i in range(NSETS):
+        for i in range(st.nsets):
             st.step(i)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     with torch.cuda.graph(graph):
-        for i in range(NSETS):
+        for i in range(st.nsets):
             st.step(i)
-    for _ in range(max(1, args.warmup // NSETS)):
+    for _ in range(max(1, args.warmup // st.nsets)):
         graph.replay()
     torch.cuda.synchronize()
     t_settle = time.perf_counter()  # untimed settling replays (steady-state clocks)
@@ -299,8 +312,8 @@ def main():
         for _ in range(20):
             graph.replay()
         torch.cuda.synchronize()
-    replays = max(1, (args.steps + NSETS - 1) // NSETS)
-    steps = replays * NSETS
+    replays = max(1, (args.steps + st.nsets - 1) // st.nsets)
+    steps = replays * st.nsets
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(replays):
@@ -312,9 +325,9 @@ def main():
     value = tokens * steps / elapsed
 
     # ---- per-launch times (graph replays of back-to-back launches)
-    t_fused, n_fused = graph_time(lambda i: st.attn(i, _lib.PHASE_ALL, fold=True))
-    t_dec, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_DECODE))
-    t_pre, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_PREFILL))
+    t_fused, n_fused = st.time(lambda i: st.attn(i, _lib.PHASE_ALL, fold=True))
+    t_dec, _ = st.time(lambda i: st.attn(i, _lib.PHASE_DECODE))
+    t_pre, _ = st.time(lambda i: st.attn(i, _lib.PHASE_PREFILL))
     fused_bytes = st.step_bytes(fold=True)
     dec_bytes = st.decode_bytes()
     flops = w.prefill_flops()
@@ -333,12 +346,12 @@ def main():
     cos_sin = rope_cos_sin(d, 40960, 1e6, device)
 
     def qk_launch(i):
-        kc, vc, ks, vs = st.pools[i % NSETS]
+        kc, vc, ks, vs = st.pools[i % st.nsets]
         qk_norm_rope_store(qkv, positions, qn_w, kn_w, 1e-6, cos_sin, hq, hkv, kc, vc, st.slots, ks, vs)
 
     # QKV row, position, cos/sin row and slot read; q, k and the K/V pool entries written
     qk_bytes = tokens * ((hq + 2 * hkv) * d * 2 + 8 + d * 4 + 4 + (hq + hkv) * d * 2 + 2 * hkv * d * 2)
-    t_qk, _ = graph_time(qk_launch)
+    t_qk, _ = st.time(qk_launch)
 
     # ---- the step after the model: LM head + greedy argmax on the step's sampled
     # rows over the Qwen3-4B head [151936, 2560]; two weight copies alternate so each
@@ -355,15 +368,16 @@ def main():
     # the reference's path on the same inputs: compute_logits (F.linear) then argmax
     t_lm_torch, _ = graph_time(lambda i: torch.nn.functional.linear(hid, heads[i % 2]).argmax(dim=-1),
                                n_per_graph=2, target=200)
+    nsets = st.nsets
     del heads, st
     torch.cuda.empty_cache()
 
     # ---- E4M3FN pool: the step (store kernel + attention launch) and the split launches
     st8 = Step(w, device, fp8=True)
-    t8_step, _ = graph_time(st8.step)
-    t8_fused, _ = graph_time(lambda i: st8.attn(i, _lib.PHASE_ALL))
-    t8_dec, _ = graph_time(lambda i: st8.attn(i, _lib.PHASE_DECODE))
-    t8_pre, _ = graph_time(lambda i: st8.attn(i, _lib.PHASE_PREFILL))
+    t8_step, _ = st8.time(st8.step)
+    t8_fused, _ = st8.time(lambda i: st8.attn(i, _lib.PHASE_ALL))
+    t8_dec, _ = st8.time(lambda i: st8.attn(i, _lib.PHASE_DECODE))
+    t8_pre, _ = st8.time(lambda i: st8.attn(i, _lib.PHASE_PREFILL))
     fp8_dec_bytes = st8.decode_bytes()
     fp8_fused_bytes = st8.step_bytes(fold=False)
     del st8
@@ -372,8 +386,8 @@ def main():
     # ---- one TP=2 rank's head shape (16 query / 4 kv heads), same rows and tables
     w2 = workloads.config(3, 16, 4)
     st2 = Step(w2, device, fp8=False)
-    t2_fused, _ = graph_time(lambda i: st2.attn(i, _lib.PHASE_ALL, fold=True))
-    t2_dec, _ = graph_time(lambda i: st2.attn(i, _lib.PHASE_DECODE))
+    t2_fused, _ = st2.time(lambda i: st2.attn(i, _lib.PHASE_ALL, fold=True))
+    t2_dec, _ = st2.time(lambda i: st2.attn(i, _lib.PHASE_DECODE))
     t2_bytes, t2_dec_bytes = st2.step_bytes(fold=True), st2.decode_bytes()
     del st2
     torch.cuda.empty_cache()
@@ -391,8 +405,8 @@ def main():
     small = {"workload": w0.name, "decode_rows": w0.num_decode, "decode_context_sum": sum(w0.decode_lens)}
     for fp8 in (False, True):
         st0 = Step(w0, device, fp8=fp8)
-        t0_step, _ = graph_time(st0.step)
-        t0_dec, _ = graph_time(lambda i: st0.attn(i, _lib.PHASE_DECODE))
+        t0_step, _ = st0.time(st0.step)
+        t0_dec, _ = st0.time(lambda i: st0.attn(i, _lib.PHASE_DECODE))
         small["e4m3fn" if fp8 else "bf16"] = {
             "step_us": round(t0_step, 2),
             "decode": hbm(st0.decode_bytes(), t0_dec, avg_launch_us=round(t0_dec, 2), decode_kv_bytes=st0.decode_bytes(),
@@ -406,7 +420,7 @@ def main():
         ceiling["decode_frac_of_lds_dma_stream"] = round(
             dec_bytes / (t_dec * 1e-6) / (ceiling["stream_lds_dma_TBps"] * 1e12), 4)
     cpu = None if args.no_cpu_baseline else cpu_baseline(w)
-    timing = f"HIP-graph replays of {NSETS} back-to-back launches over {NSETS} pool copies; us per launch"
+    timing = f"HIP-graph replays of {nsets} back-to-back launches over {nsets} pool copies; us per launch"
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -425,7 +439,7 @@ def main():
             "prefill_chunks": w.prefill_q, "prefill_prefixes": w.prefill_prefix, "new_tokens": tokens,
             "heads": [hq, hkv, d], "block_size": w.block_size, "kv_cache": "bf16",
             "step": "one fused ragged attention launch with the KV write folded in (forward_mixed)",
-            "pool_copies_rotated": NSETS,
+            "pool_copies_rotated": nsets,
         },
         "roofline": hbm(fused_bytes, t_fused, traffic=traffic_of("fused"),
                         kernel="paged_attention_kernel (fused decode+prefill, KV write folded in)",
@@ -497,7 +511,7 @@ def profile(args, device):
         cs = rope_cos_sin(st.d, 4096, 1e6, device)
 
         def launch(i):
-            kc, vc, ks, vs = st.pools[i % NSETS]
+            kc, vc, ks, vs = st.pools[i % st.nsets]
             qk_norm_rope_store(qkv, pos, ones, ones, 1e-6, cs, st.hq, st.hkv, kc, vc, st.slots, ks, vs)
     else:
         heads = [torch.empty(151936, 2560, dtype=torch.bfloat16, device=device).normal_(0, 0.02) for _ in range(2)]
@@ -534,17 +548,17 @@ def config_table(args, device):
         for fp8 in (False, True):
             st = Step(w, device, fp8=fp8)
             r = {}
-            t, _ = graph_time(st.step)
+            t, _ = st.time(st.step)
             r["step_us"] = round(t, 2)
             r["step_tokens_per_s"] = round(w.num_tokens / (t * 1e-6), 1)
             if w.num_decode:
-                t, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_DECODE))
+                t, _ = st.time(lambda i: st.attn(i, _lib.PHASE_DECODE))
                 r["decode_us"] = round(t, 2)
                 r["decode_kv_bytes"] = st.decode_bytes()
                 r["decode_GBps"] = round(st.decode_bytes() / (t * 1e-6) / 1e9, 1)
                 r["decode_frac_hbm"] = round(st.decode_bytes() / (t * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
             if w.prefill_q:
-                t, _ = graph_time(lambda i: st.attn(i, _lib.PHASE_PREFILL))
+                t, _ = st.time(lambda i: st.attn(i, _lib.PHASE_PREFILL))
                 r["prefill_us"] = round(t, 2)
                 r["prefill_TFLOPs"] = round(w.prefill_flops() / (t * 1e-6) / 1e12, 1)
                 r["prefill_frac_mfma"] = round(w.prefill_flops() / (t * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)

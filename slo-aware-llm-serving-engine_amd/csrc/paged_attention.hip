@@ -213,6 +213,7 @@ struct Smem {
   int pf_ticket;    // prefill split item: ticket value before this item's arrival
   int meta[2][20];  // decode: landed row length and block-table entries, by item parity
   int bcast[2];     // decode: row and local index of the item fetched by wavefront 0
+  int kv_nt;        // decode K/V loads with the non-temporal cache policy
 };
 
 
@@ -534,8 +535,10 @@ __device__ __forceinline__ void decode_issue_q(const Params& p, uint8_t* qbuf, c
 // K and V of one wavefront step to the wavefront's stage region `stg`.
 // bf16: K row r at r*ROWB with 16-byte chunk c in slot c ^ (r & 15), V rows
 // from 4*ROWB*4 on with chunk c in slot c ^ 2*(r & 7).  E4M3FN (32 tokens):
-// see below; the scales go to `scl`.
-template <bool FP8, bool FOLD>
+// see below; the scales go to `scl`.  NT: the K/V (code) bytes are loaded
+// with the non-temporal cache policy, which streams them faster (each line is
+// read once, whole).
+template <bool FP8, bool FOLD, bool NT = true>
 __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, float* scl, uint8_t* nrw, const DMeta& m,
                                              int s, int wave, int lane) {
   const int n = lane & 15, g = lane >> 4;
@@ -563,16 +566,23 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, floa
     const int tnew = FOLD ? decode_L(p, m) - 1 - t0 : -1;  // its row in this step, if any
     const uint16_t* kn = FOLD ? p.nk + (int64_t)m.b * p.nk_stride + m.h * HD : kc;
     const uint16_t* vn = FOLD ? p.nv + (int64_t)m.b * p.nv_stride + m.h * HD : vc;
+    auto load = [&](auto policy_nt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * i + g;
-      dma16((r == tnew ? kn : kc + r * row) + 8 * (n ^ (r & 15)), dst + i * 1024);
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + g;
+        const uint16_t* src = (r == tnew ? kn : kc + r * row) + 8 * (n ^ (r & 15));
+        if constexpr (decltype(policy_nt)::value) dma16_nt(src, dst + i * 1024);
+        else dma16(src, dst + i * 1024);
+      }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * i + g;
-      dma16((r == tnew ? vn : vc + r * row) + 8 * (n ^ ((r & 7) << 1)), dst + DT * ROWB + i * 1024);
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + g;
+        const uint16_t* src = (r == tnew ? vn : vc + r * row) + 8 * (n ^ ((r & 7) << 1));
+        if constexpr (decltype(policy_nt)::value) dma16_nt(src, dst + DT * ROWB + i * 1024);
+        else dma16(src, dst + DT * ROWB + i * 1024);
+      }
+    };
+    load(std::integral_constant<bool, NT>());
   } else {
     // 32 tokens: rows 16h..16h+15 go to half h at 4096h (K codes, 128-byte
     // rows with 16-byte chunk c in slot c ^ (r & 7), then V codes at +2048);
@@ -580,16 +590,23 @@ __device__ __forceinline__ void decode_issue(const Params& p, uint8_t* stg, floa
     const uint8_t* kc = static_cast<const uint8_t*>(p.k_cache) + base;
     const uint8_t* vc = static_cast<const uint8_t*>(p.v_cache) + base;
     const uint32_t dst = lds_addr(stg);
+    auto load = [&](auto policy_nt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 8 * i + (lane >> 3);
-      dma16(kc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + (i >> 1) * 4096 + (i & 1) * 1024);
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const uint8_t* src = kc + r * row + 16 * ((lane & 7) ^ (r & 7));
+        if constexpr (decltype(policy_nt)::value) dma16_nt(src, dst + (i >> 1) * 4096 + (i & 1) * 1024);
+        else dma16(src, dst + (i >> 1) * 4096 + (i & 1) * 1024);
+      }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 8 * i + (lane >> 3);
-      dma16(vc + r * row + 16 * ((lane & 7) ^ (r & 7)), dst + (i >> 1) * 4096 + 2048 + (i & 1) * 1024);
-    }
+      for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        const uint8_t* src = vc + r * row + 16 * ((lane & 7) ^ (r & 7));
+        if constexpr (decltype(policy_nt)::value) dma16_nt(src, dst + (i >> 1) * 4096 + 2048 + (i & 1) * 1024);
+        else dma16(src, dst + (i >> 1) * 4096 + 2048 + (i & 1) * 1024);
+      }
+    };
+    load(std::integral_constant<bool, NT>());
     const float* sc = (lane & 32) ? p.v_scale : p.k_scale;
     dma4(sc + (slot0 + (lane & 31)) * p.hkv + m.h, lds_addr(scl));
     if constexpr (FOLD) {
@@ -1092,7 +1109,7 @@ __device__ __forceinline__ void wait_vm(int extra) {
 // nxt is learned at step 1 from the fetch issued at the end of the previous
 // item, so a workgroup holds at most its current item and one claimed item
 // that has not started.
-template <bool FP8, bool FOLD>
+template <bool FP8, bool FOLD, bool NT>
 __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1, uint8_t* qbuf, int list, int nlist,
                            uint32_t count, uint32_t base, uint32_t* ctr, int decode_base, int nrows, uint32_t rel0,
                            int r0, int dchunk, int tid) {
@@ -1126,10 +1143,10 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
   lds_sync();
   decode_meta_read<FP8>(cur, sm, 0, wave);
   decode_issue_q(p, qbuf, cur, wave, lane);
-  decode_issue<FP8, FOLD>(p, sa, ca, na, cur, 0, wave, lane);
+  decode_issue<FP8, FOLD, NT>(p, sa, ca, na, cur, 0, wave, lane);
   for (int i = 0; i < hgp; ++i)
     if (lane < 33) store16(reinterpret_cast<uint8_t*>(p.ctrl) + TRASH_OFFSET + 16 * lane, u32x4{0, 0, 0, 0});
-  decode_issue<FP8, FOLD>(p, sb, cb, nb, cur, 1, wave, lane);
+  decode_issue<FP8, FOLD, NT>(p, sb, cb, nb, cur, 1, wave, lane);
   uint32_t f = 0;
   bool fetching = true;  // the fetch in flight is a real one
   if (tid == 0) f = atomic_add_ret(ctr, 1u);
@@ -1154,7 +1171,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0, 0, 0, 0};
     float m = NEG_INF, l = 0.0f;
     decode_wstep<FP8, FOLD>(p, sa, ca, na, decode_ntok<FP8>(p, cur, 0, wave), tnew_of(cur, 0), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, ca, na, cur, 2, wave, lane);
+    decode_issue<FP8, FOLD, NT>(p, sa, ca, na, cur, 2, wave, lane);
 
     // Step 1: (cur, 1) has landed, and with it prev's stores (every
     // wavefront's, after the barrier) and the fetch.  Wavefront 0 finds the
@@ -1184,7 +1201,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       decode_meta_dma<FP8>(p, sm, nxt, (k + 1) & 1, lane);
     }
     decode_wstep<FP8, FOLD>(p, sb, cb, nb, decode_ntok<FP8>(p, cur, 1, wave), tnew_of(cur, 1), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sb, cb, nb, cur, 3, wave, lane);
+    decode_issue<FP8, FOLD, NT>(p, sb, cb, nb, cur, 3, wave, lane);
 
     // Step 2: (cur, 2) and nxt's metadata have landed; the broadcast is
     // visible after the barrier.
@@ -1204,7 +1221,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
     decode_issue_q(p, qnxt, nxt, wave, lane);
     if (!half)
       decode_wstep<FP8, FOLD>(p, sa, ca, na, decode_ntok<FP8>(p, cur, 2, wave), tnew_of(cur, 2), qv, o, m, l, lane);
-    decode_issue<FP8, FOLD>(p, sa, ca, na, nxt, 0, wave, lane);
+    decode_issue<FP8, FOLD, NT>(p, sa, ca, na, nxt, 0, wave, lane);
 
     // Step 3: (cur, 3) has landed.
     wait_vm<GROUP + 1>(0);
@@ -1212,7 +1229,7 @@ __device__ void decode_run(const Params& p, Smem& sm, uint8_t* st0, uint8_t* st1
       decode_wstep<FP8, FOLD>(p, sb, cb, nb, decode_ntok<FP8>(p, cur, 3, wave), tnew_of(cur, 3), qv, o, m, l, lane);
     lds_sync();  // every wavefront's last step is done: merge area and stage-1 regions are free
     decode_merge(p, sm, st1, cur, tid, o, m, l);
-    decode_issue<FP8, FOLD>(p, sb, cb, nb, nxt, 1, wave, lane);
+    decode_issue<FP8, FOLD, NT>(p, sb, cb, nb, nxt, 1, wave, lane);
     fetching = fetching && has1;
     if (tid == 0) f = atomic_add_ret(ctr, fetching ? 1u : 0u);
     prev = cur;
@@ -2034,6 +2051,12 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // short launches (about three items per workgroup) ran 3% slower
       // with it.
       sm.drot = dt * p.hkv >= 6 * (int64_t)gridDim.x;
+      // Non-temporal K/V loads stream faster, but in mixed launches whose
+      // prefill items are the critical path (decode work under 4 times the
+      // prefill work) they made the launch slower: 24 decode rows of
+      // 256-4096 tokens with two 512-token chunks 65.8 -> 66.5 us, while 64
+      // rows of 512-4096 with one 1,024-token chunk went 146.4 -> 137.6 us.
+      sm.kv_nt = MODE != MODE_MIXED || 4 * dt * p.hkv >= 4 * wt;
       sm.pf_split_thr = MODE == MODE_PREFILL ? (int)max((int64_t)16, 2 * wt / gridDim.x) : (1 << 30);
     }
     __syncthreads();
@@ -2271,9 +2294,14 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
         continue;
       }
       // The rest of this decode list is one streaming decode run.
-      if constexpr (HAS_DEC)
-        decode_run<FP8, FOLD>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows, rel, r,
-                              dchunk, ltid);
+      if constexpr (HAS_DEC) {
+        if (MODE == MODE_DECODE || sm.kv_nt)
+          decode_run<FP8, FOLD, true>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows,
+                                      rel, r, dchunk, ltid);
+        else
+          decode_run<FP8, FOLD, false>(p, sm, stage0, stage1, qbuf, list, nlist, count, base, ctr, decode_base, nrows,
+                                       rel, r, dchunk, ltid);
+      }
       break;
     }
     if (tid == 0 && sm.item == count + wgs - 1u) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
