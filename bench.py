@@ -41,8 +41,12 @@ device synchronisations.
 * roofline_decode.read_ceiling: what a plain read of the same byte count
   achieves on this GPU (read_ceiling, built from read_ceiling.hip next to
   this file by __graft_entry__.build(), run as a child process: one-pass
-  streams into VGPRs and through LDS-DMA, the decode kernels' route), and
-  the decode launch's rate as a fraction of the LDS-DMA stream.
+  streams into VGPRs and through LDS-DMA with the default and the
+  non-temporal cache policy, the last the decode kernels' route), and the
+  decode launch's rate as a fraction of that non-temporal LDS-DMA stream.
+* Pool copies: enough are rotated that the launches read at least twice the
+  MI355X Infinity Cache (256 MiB) between two visits of one copy, so the KV
+  bytes come from HBM (4 copies for the config-3 step, 17 for config 0).
 * cpu_baseline: the CPU oracle (fp32 PyTorch on the host cores) on the same
   step, median of 5 runs after 1 warm-up.
 """
@@ -417,8 +421,9 @@ def main():
 
     ceiling = read_ceiling(dec_bytes)
     if ceiling:
+        # The decode kernels stream K/V by non-temporal LDS-DMA.
         ceiling["decode_frac_of_lds_dma_stream"] = round(
-            dec_bytes / (t_dec * 1e-6) / (ceiling["stream_lds_dma_TBps"] * 1e12), 4)
+            dec_bytes / (t_dec * 1e-6) / (ceiling.get("stream_lds_dma_nt_TBps", ceiling["stream_lds_dma_TBps"]) * 1e12), 4)
     cpu = None if args.no_cpu_baseline else cpu_baseline(w)
     timing = f"HIP-graph replays of {nsets} back-to-back launches over {nsets} pool copies; us per launch"
     line = {

@@ -5,8 +5,9 @@
 //  * stream: BYTES read once from HBM (four rotated copies, so no launch finds
 //    its bytes in L2 or the memory-side cache), split evenly over the grid,
 //    16 bytes per lane per access, 8 accesses in flight per lane, either into
-//    VGPRs (global_load_dwordx4) or straight into LDS (global_load_lds_dwordx4,
-//    the route the decode kernels take);
+//    VGPRs (global_load_dwordx4, non-temporal) or straight into LDS
+//    (global_load_lds_dwordx4) with the default cache policy and with the
+//    non-temporal one (the route the decode kernels take);
 //  * tiles: the prefill tile pattern, 64 pool rows x 256 bytes (one kv head's
 //    slice of a 2 KiB row) for K and for V per tile, double-buffered into LDS
 //    by 512 workgroups; the workgroups of one XCD (b % 8) all read one kv
@@ -45,6 +46,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(
 __device__ __forceinline__ void dma16(const void* gp, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gp), "s"(lds) : "memory", "m0");
 }
+__device__ __forceinline__ void dma16_nt(const void* gp, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gp), "s"(lds) : "memory", "m0");
+}
 
 __device__ __forceinline__ uint64_t lds_tr16(const uint8_t* p) {
   typedef short v4s __attribute__((ext_vector_type(4)));
@@ -53,7 +57,7 @@ __device__ __forceinline__ uint64_t lds_tr16(const uint8_t* p) {
 }
 
 // Workgroup b reads [b * per, (b + 1) * per) of `base` (per: a multiple of 4 KiB).
-template <bool LDS>
+template <bool LDS, bool NTP = false>
 __global__ void __launch_bounds__(NT) stream_kernel(const uint8_t* base, uint64_t per, uint32_t* sink) {
   __shared__ __attribute__((aligned(1024))) uint8_t stage[4 * DEPTH * 1024];
   const int tid = threadIdx.x, wave = tid >> 6;
@@ -64,9 +68,11 @@ __global__ void __launch_bounds__(NT) stream_kernel(const uint8_t* base, uint64_
     if constexpr (LDS) {
 #pragma unroll
       for (int j = 0; j < DEPTH; ++j)
-        if (i + j < pieces)
-          dma16(src + (uint64_t)(i + j) * NT * 16,
-                __builtin_amdgcn_readfirstlane(lds_addr(stage + (wave * DEPTH + j) * 1024)));
+        if (i + j < pieces) {
+          const uint32_t dl = __builtin_amdgcn_readfirstlane(lds_addr(stage + (wave * DEPTH + j) * 1024));
+          if constexpr (NTP) dma16_nt(src + (uint64_t)(i + j) * NT * 16, dl);
+          else dma16(src + (uint64_t)(i + j) * NT * 16, dl);
+        }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
       u32x4 v[DEPTH];
@@ -153,15 +159,16 @@ int main(int argc, char** argv) {
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  double best[4] = {1e30, 1e30, 1e30, 1e30};
-  for (int kind = 0; kind < 4; ++kind) {
+  double best[5] = {1e30, 1e30, 1e30, 1e30, 1e30};
+  for (int kind = 0; kind < 5; ++kind) {
     for (int rep = 0; rep < 12; ++rep) {
       const uint8_t* base = buf + (uint64_t)(rep % 4) * copy_stride;
       CHECK(hipEventRecord(e0));
       if (kind == 0) stream_kernel<false><<<grid, NT>>>(base, per, sink);
       else if (kind == 1) stream_kernel<true><<<grid, NT>>>(base, per, sink);
       else if (kind == 2) tile_kernel<false><<<grid, NT>>>(buf, rows, ntiles, sink);
-      else tile_kernel<true><<<grid, NT>>>(buf, rows, ntiles, sink);
+      else if (kind == 3) tile_kernel<true><<<grid, NT>>>(buf, rows, ntiles, sink);
+      else stream_kernel<true, true><<<grid, NT>>>(base, per, sink);
       CHECK(hipEventRecord(e1));
       CHECK(hipEventSynchronize(e1));
       float ms = 0.0f;
@@ -173,10 +180,12 @@ int main(int argc, char** argv) {
   const double tiles = (double)grid * ntiles * 32768;
   std::printf(
       "{\"bytes\": %llu, \"stream_vgpr_us\": %.2f, \"stream_vgpr_TBps\": %.3f, \"stream_lds_dma_us\": %.2f, "
-      "\"stream_lds_dma_TBps\": %.3f, \"tile_fill_TBps\": %.2f, \"tile_us_per_workgroup\": %.3f, "
+      "\"stream_lds_dma_TBps\": %.3f, \"stream_lds_dma_nt_us\": %.2f, \"stream_lds_dma_nt_TBps\": %.3f, "
+      "\"tile_fill_TBps\": %.2f, \"tile_us_per_workgroup\": %.3f, "
       "\"tile_fill_with_operand_reads_TBps\": %.2f, \"tile_with_operand_reads_us_per_workgroup\": %.3f}\n",
       (unsigned long long)copy, best[0] * 1e3, copy / (best[0] * 1e-3) / 1e12, best[1] * 1e3,
-      copy / (best[1] * 1e-3) / 1e12, tiles / (best[2] * 1e-3) / 1e12, best[2] * 1e3 / ntiles,
+      copy / (best[1] * 1e-3) / 1e12, best[4] * 1e3, copy / (best[4] * 1e-3) / 1e12, tiles / (best[2] * 1e-3) / 1e12,
+      best[2] * 1e3 / ntiles,
       tiles / (best[3] * 1e-3) / 1e12, best[3] * 1e3 / ntiles);
   return 0;
 }
