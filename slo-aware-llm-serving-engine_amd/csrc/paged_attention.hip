@@ -1338,7 +1338,7 @@ constexpr int DIRECT_ENTRIES = 32;  // block-table entries of a direct chunk (at
 // workgroups also copy the new rows to their slots (nothing in the launch
 // reads those slots: a decode row's newest token comes from its new row).
 template <bool FP8, bool FOLD>
-__global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_cap, int ns) {
+__global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_cap, int ns, int spread) {
   __shared__ Smem sm;
   __shared__ int dmeta[1 + DIRECT_ENTRIES];  // row length, then the chunk's block-table entries
   __shared__ __attribute__((aligned(16))) uint8_t stage0[4 * WSTAGE];
@@ -1373,8 +1373,18 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
     return any;
   };
 
+  // With `spread` (bf16 pools, kv heads a multiple of the 8 XCDs, at most
+  // two rounds of workgroups) the kv heads of a group are consecutive
+  // workgroups instead, on different XCDs: XCD k reads kv heads k, k + 8, ...
+  // of every group, each 256-byte slice of a 2 KiB pool row at about the time
+  // the other XCDs read the row's other slices (24 rows of 256-4096 tokens
+  // 45.4 -> 43.9 us; 16 rows of 64-1,024 14.9 -> 14.7 us).  Longer launches,
+  // whose rounds drift apart, and fewer kv heads keep the mapping above (64
+  // rows of 512-4096 tokens measured 125.2 -> 128.1 us spread, 24 rows at 4
+  // kv heads 26.8 -> 31.6 us).
+  const bool spr = !FP8 && spread;
   const int jx = x / (8 * p.hkv);
-  const int grp = jx * 8 + (x + jx) % 8;
+  const int grp = spr ? x / p.hkv : jx * 8 + (x + jx) % 8;
   if (grp >= nch_cap * p.nd) {
     side_work();
     return;
@@ -1382,7 +1392,7 @@ __global__ void __launch_bounds__(NT, 2) decode_direct_kernel(Params p, int nch_
   DMeta m;
   m.c = grp / p.nd;
   m.b = grp % p.nd;
-  m.h = (x / 8) % p.hkv;
+  m.h = spr ? x % p.hkv : (x / 8) % p.hkv;
   m.dindex = (m.b * nch_cap + m.c) * p.hkv + m.h;
   m.span = ns * d_step<FP8>();
   m.tok0 = m.c * m.span;
@@ -2340,7 +2350,7 @@ AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
   return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
 }
 
-using DirectKernel = void (*)(Params, int, int);
+using DirectKernel = void (*)(Params, int, int, int);
 DirectKernel direct_kernel(bool fold, bool fp8) {
   static const DirectKernel table[2][2] = {{decode_direct_kernel<false, false>, decode_direct_kernel<true, false>},
                                            {decode_direct_kernel<false, true>, decode_direct_kernel<true, true>}};
@@ -2623,7 +2633,8 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
       const int nch_cap = std::max(1, (dec_len_cap + ch - 1) / ch);
       const int64_t dgrid = ((int64_t)p.nd * nch_cap + 7) / 8 * 8 * p.hkv;
       if (dgrid > (steps == max_steps ? DIRECT_MAX_ROUNDS[kfp8 ? 1 : 0] * held : held + held / 2)) continue;
-      void* dargs[] = {&p, const_cast<int*>(&nch_cap), &steps};
+      int spread = !kfp8 && p.hkv % 8 == 0 && dgrid <= 2 * held ? 1 : 0;
+      void* dargs[] = {&p, const_cast<int*>(&nch_cap), &steps, &spread};
       if (hipLaunchKernel(reinterpret_cast<const void*>(direct_kernel(fold, kfp8)), dim3((unsigned)dgrid), dim3(NT),
                           dargs, 0, static_cast<hipStream_t>(stream)) != hipSuccess)
         return fail(SLO_ERR_HIP, "paged_attention: launch failed");
