@@ -42,8 +42,11 @@ device synchronisations.
   achieves on this GPU (read_ceiling, built from read_ceiling.hip next to
   this file by __graft_entry__.build(), run as a child process: one-pass
   streams into VGPRs and through LDS-DMA with the default and the
-  non-temporal cache policy, the last the decode kernels' route), and the
-  decode launch's rate as a fraction of that non-temporal LDS-DMA stream.
+  non-temporal cache policy, the last the decode kernels' route, and the
+  decode kernels' access pattern: one kv head's 256-byte slice of each 2 KiB
+  pool row), and the decode launch's rate as a fraction of the non-temporal
+  LDS-DMA stream and of the head-slice read with the kv heads of a row range
+  on different XCDs (the mapping the config-3 decode launch takes).
 * Pool copies: enough are rotated that the launches read at least twice the
   MI355X Infinity Cache (256 MiB) between two visits of one copy, so the KV
   bytes come from HBM (4 copies for the config-3 step, 17 for config 0).
@@ -424,6 +427,9 @@ def main():
         # The decode kernels stream K/V by non-temporal LDS-DMA.
         ceiling["decode_frac_of_lds_dma_stream"] = round(
             dec_bytes / (t_dec * 1e-6) / (ceiling.get("stream_lds_dma_nt_TBps", ceiling["stream_lds_dma_TBps"]) * 1e12), 4)
+        if ceiling.get("head_slices_spread_TBps"):
+            ceiling["decode_frac_of_head_slice_stream"] = round(
+                dec_bytes / (t_dec * 1e-6) / (ceiling["head_slices_spread_TBps"] * 1e12), 4)
     cpu = None if args.no_cpu_baseline else cpu_baseline(w)
     timing = f"HIP-graph replays of {nsets} back-to-back launches over {nsets} pool copies; us per launch"
     line = {

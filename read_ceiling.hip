@@ -8,6 +8,12 @@
 //    VGPRs (global_load_dwordx4, non-temporal) or straight into LDS
 //    (global_load_lds_dwordx4) with the default cache policy and with the
 //    non-temporal one (the route the decode kernels take);
+//  * head slices: the decode kernels' pattern over the same bytes taken as
+//    pool rows of 8 kv heads x 256 bytes: each workgroup reads one head's
+//    256-byte slice of consecutive rows by non-temporal LDS-DMA (4 rows per
+//    instruction, two steps of 16 rows per wavefront in flight), the 8 heads
+//    of a row range either on workgroups b, b + 8, ..., b + 56 (one XCD) or
+//    on consecutive workgroups (eight XCDs);
 //  * tiles: the prefill tile pattern, 64 pool rows x 256 bytes (one kv head's
 //    slice of a 2 KiB row) for K and for V per tile, double-buffered into LDS
 //    by 512 workgroups; the workgroups of one XCD (b % 8) all read one kv
@@ -92,6 +98,31 @@ __global__ void __launch_bounds__(NT) stream_kernel(const uint8_t* base, uint64_
   sink[blockIdx.x * NT + tid] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
 
+// Head slices of 2 KiB rows: workgroup b reads head h's 256 bytes of rows
+// [grp * rows_per, (grp + 1) * rows_per).  SPREAD: h = b % 8, grp = b / 8;
+// otherwise h = (b / 8) % 8, grp = (b / 64) * 8 + b % 8.
+template <bool SPREAD>
+__global__ void __launch_bounds__(NT) slice_kernel(const uint8_t* base, int rows_per, uint32_t* sink) {
+  __shared__ __attribute__((aligned(1024))) uint8_t stage[2][4][4096];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, b = blockIdx.x;
+  const int h = SPREAD ? b % 8 : (b / 8) % 8;
+  const int grp = SPREAD ? b / 8 : (b / 64) * 8 + b % 8;
+  const uint8_t* rows = base + (uint64_t)grp * rows_per * 2048 + 256 * h;
+  const int g = lane >> 4, n = lane & 15;
+  for (int s = 0; s < rows_per / 64; ++s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = s * 64 + wave * 16 + 4 * i + g;
+      dma16_nt(rows + (uint64_t)r * 2048 + 16 * n,
+               __builtin_amdgcn_readfirstlane(lds_addr(stage[s & 1][wave] + 1024 * i)));
+    }
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // step s - 1 landed, step s in flight
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  sink[b * NT + tid] = reinterpret_cast<const uint32_t*>(stage)[tid];
+}
+
 // Tile t of workgroup b: pool rows 64 * ((t + b / 8) % (rows / 64)) onwards,
 // kv head b % 8; K rows at `pool`, V rows `rows` rows later.  READS: every
 // wavefront reads the landed tile's K (first 16 KiB) and V (last 16 KiB).
@@ -159,8 +190,11 @@ int main(int argc, char** argv) {
   hipEvent_t e0, e1;
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
-  double best[5] = {1e30, 1e30, 1e30, 1e30, 1e30};
-  for (int kind = 0; kind < 5; ++kind) {
+  // Head slices: 64 row ranges of rows_per 2 KiB rows within one copy.
+  const int rows_per = (int)(copy / 2048 / 64 / 64 * 64);
+  const double slices = (double)grid * rows_per * 256;
+  double best[7] = {1e30, 1e30, 1e30, 1e30, 1e30, 1e30, 1e30};
+  for (int kind = 0; kind < 7; ++kind) {
     for (int rep = 0; rep < 12; ++rep) {
       const uint8_t* base = buf + (uint64_t)(rep % 4) * copy_stride;
       CHECK(hipEventRecord(e0));
@@ -168,7 +202,9 @@ int main(int argc, char** argv) {
       else if (kind == 1) stream_kernel<true><<<grid, NT>>>(base, per, sink);
       else if (kind == 2) tile_kernel<false><<<grid, NT>>>(buf, rows, ntiles, sink);
       else if (kind == 3) tile_kernel<true><<<grid, NT>>>(buf, rows, ntiles, sink);
-      else stream_kernel<true, true><<<grid, NT>>>(base, per, sink);
+      else if (kind == 4) stream_kernel<true, true><<<grid, NT>>>(base, per, sink);
+      else if (kind == 5) slice_kernel<false><<<grid, NT>>>(base, rows_per, sink);
+      else slice_kernel<true><<<grid, NT>>>(base, rows_per, sink);
       CHECK(hipEventRecord(e1));
       CHECK(hipEventSynchronize(e1));
       float ms = 0.0f;
@@ -181,11 +217,14 @@ int main(int argc, char** argv) {
   std::printf(
       "{\"bytes\": %llu, \"stream_vgpr_us\": %.2f, \"stream_vgpr_TBps\": %.3f, \"stream_lds_dma_us\": %.2f, "
       "\"stream_lds_dma_TBps\": %.3f, \"stream_lds_dma_nt_us\": %.2f, \"stream_lds_dma_nt_TBps\": %.3f, "
+      "\"head_slice_bytes\": %.0f, \"head_slices_one_xcd_us\": %.2f, \"head_slices_one_xcd_TBps\": %.3f, "
+      "\"head_slices_spread_us\": %.2f, \"head_slices_spread_TBps\": %.3f, "
       "\"tile_fill_TBps\": %.2f, \"tile_us_per_workgroup\": %.3f, "
       "\"tile_fill_with_operand_reads_TBps\": %.2f, \"tile_with_operand_reads_us_per_workgroup\": %.3f}\n",
       (unsigned long long)copy, best[0] * 1e3, copy / (best[0] * 1e-3) / 1e12, best[1] * 1e3,
-      copy / (best[1] * 1e-3) / 1e12, best[4] * 1e3, copy / (best[4] * 1e-3) / 1e12, tiles / (best[2] * 1e-3) / 1e12,
-      best[2] * 1e3 / ntiles,
-      tiles / (best[3] * 1e-3) / 1e12, best[3] * 1e3 / ntiles);
+      copy / (best[1] * 1e-3) / 1e12, best[4] * 1e3, copy / (best[4] * 1e-3) / 1e12, slices, best[5] * 1e3,
+      slices / (best[5] * 1e-3) / 1e12, best[6] * 1e3, slices / (best[6] * 1e-3) / 1e12,
+      tiles / (best[2] * 1e-3) / 1e12, best[2] * 1e3 / ntiles, tiles / (best[3] * 1e-3) / 1e12,
+      best[3] * 1e3 / ntiles);
   return 0;
 }
