@@ -202,6 +202,7 @@ struct Smem {
   int off[MAX_ROWS + 1];
   int wsum[4];
   int wmax[4];
+  int wumax[4];     // prefill-only set-up: key tiles of the longest block of a row that cannot split
   int dsum[4];
   uint32_t item;
   int row;
@@ -325,10 +326,12 @@ __device__ __forceinline__ PfRow pf_row(const Params& p, int r) {
 
 // Key tiles of the heaviest 32-position block of a prefill row, and an
 // estimate of the row's total tile work (blocks x mean tiles x kv heads x
-// head groups).
-__device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& tmax) {
+// head groups); `long_prefix`, when given, is set to whether the row's cached
+// prefix is at least as long as its chunk (such rows may split, pf_splits).
+__device__ __forceinline__ void pf_work(const Params& p, int r, int& work, int& tmax, bool* long_prefix = nullptr) {
   const PfRow g = pf_row(p, r);
   work = tmax = 0;
+  if (long_prefix) *long_prefix = g.Lq > 0 && g.prefix >= g.Lq;
   if (g.Lq <= 0) return;
   const int nqb = (g.Lq + 31) / 32;
   tmax = (min(g.Lk, max(0, g.prefix + g.Lq)) + TT - 1) / TT;
@@ -1971,7 +1974,8 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // (the decode work hides the longest prefill item and 32 halves the key
   // tiles loaded per query); a prefill-only launch uses 16 when the heaviest
   // 32-position block would take more than twice a workgroup's fair share of
-  // the work (the launch would wait on that one item), else 32.  Decode chunk:
+  // the work (the launch would wait on that one item) and not every such row
+  // splits its keys (below), else 32.  Decode chunk:
   // d_chunk tokens (bf16 256, E4M3FN 512) when that still gives at least two
   // items per workgroup, else half of it (bf16 only: short launches need the
   // parallelism more than the longer items' lower per-token overhead).
@@ -1984,8 +1988,12 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   // was compiled into a load through a selected address, which kept both
   // arrays in scratch memory.
   int cnt_a[4], cnt_d[4], tmr[4];
+  bool pf_long = false;  // prefill-only: a 32-position block spans over twice a workgroup's share
   {
-    int w = 0, tm = 0, dn = 0;
+    // tu: the longest block of this thread's rows that cannot split (a
+    // short prefix, or at most 16 key tiles: pf_splits); a long row with more
+    // than 16 tiles and a long prefix splits whenever it is long.
+    int w = 0, tm = 0, dn = 0, tu = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = r0 + i;
@@ -1994,7 +2002,9 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       if (i >= per || r >= nrows) continue;
       if (r < p.np) {
         int wr, tr;
-        pf_work(p, r, wr, tr);
+        bool lp = false;
+        pf_work(p, r, wr, tr, &lp);
+        if (!lp || tr <= 16) tu = max(tu, tr);
         w += wr;
         tm = max(tm, tr);
         tmr[i] = tr;
@@ -2014,22 +2024,35 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       w += __shfl_xor(w, d, 64);
       tm = max(tm, __shfl_xor(tm, d, 64));
       dn += __shfl_xor(dn, d, 64);
+      if constexpr (MODE == MODE_PREFILL && !FOLD) tu = max(tu, __shfl_xor(tu, d, 64));
     }
     if (lane == 0) {
       sm.wsum[wave] = w;
       sm.wmax[wave] = tm;
       sm.dsum[wave] = dn;
+      sm.wumax[wave] = tu;
     }
     __syncthreads();
     int64_t wt = 0, dt = 0;
-    int tmax = 0;
+    int tmax = 0, tunsplit = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       wt += sm.wsum[i];
       tmax = max(tmax, sm.wmax[i]);
       dt += sm.dsum[i];
+      tunsplit = max(tunsplit, sm.wumax[i]);
     }
-    if (MODE == MODE_PREFILL && (int64_t)tmax * gridDim.x > 2 * wt) bq = 16;
+    pf_long = MODE == MODE_PREFILL && (int64_t)tmax * gridDim.x > 2 * wt;
+    if (pf_long) {
+      // Rows that split their keys in two (below) halve their longest items
+      // already, and take 32-position blocks, whose tiles cost half the LDS
+      // operand reads per query (three 512-token chunks after prefixes
+      // 0/2048/512: 65.6 -> 50.9 us; two after 0 and 1,024: 38.0 -> 37.3
+      // us); the other rows take 16 only when one of them is this long.  The
+      // folded instantiation keeps 16 for all (its 32-position split items
+      // would spill registers).
+      if (FOLD || (int64_t)tunsplit * gridDim.x > 2 * wt) bq = 16;
+    }
     // (E4M3FN launches always take full 512-token items: measured 27.0 ->
     // 25.5 us on 16 rows of 64-1024 tokens and 54 -> 51 us on 24 rows of
     // 256-4096, where half items keep half the bytes in flight.)
@@ -2083,9 +2106,11 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (i >= per || r0 + i >= nrows) continue;
-      const int c = cnt_a[i] + (bq == 16 ? cnt_d[i] : 0);
+      // Split rows take 32-position blocks except in the folded instantiation.
+      const bool sp = pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr);
+      const int c = cnt_a[i] + (bq == 16 && !(sp && !FOLD) ? cnt_d[i] : 0);
       base_c += c;
-      if (pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) extra_c += c;
+      if (sp) extra_c += c;
     }
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -2100,10 +2125,13 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
     if (tid == 0) {
       const int all = sm.wsum[0] + sm.wsum[1] + sm.wsum[2] + sm.wsum[3];
       const int ext = sm.dsum[0] + sm.dsum[1] + sm.dsum[2] + sm.dsum[3];
-      const int cap = (int)(p.pf_split_bytes / (int64_t)(sizeof(float) * (size_t)PF_REC_FLOATS * (bq / 16)));
+      // Record slots of 32-position items (16 in the folded instantiation).
+      const int cap = (int)(p.pf_split_bytes / (int64_t)(sizeof(float) * (size_t)PF_REC_FLOATS * (FOLD ? bq / 16 : 2)));
       if (ext == 0 || all + ext > cap || all + ext > MAX_COUNTERS) sm.pf_split_thr = 1 << 30;
     }
     __syncthreads();
+    // No split after all: long rows take 16-position blocks.
+    if (sm.pf_split_thr == (1 << 30) && pf_long) bq = 16;
   }
 
   // Per-row item counts -> exclusive prefix in sm.off (block-wide scan).
@@ -2111,9 +2139,11 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
   int local_sum = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const bool alt = r0 + i < p.np ? (bq == 16 || tmr[i] > sm.split_tiles) : dchunk == d_chunk_min<FP8>();
+    const bool sp = MODE == MODE_PREFILL && r0 + i < p.np && pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr);
+    const bool alt = r0 + i < p.np ? ((bq == 16 && !(sp && !FOLD)) || tmr[i] > sm.split_tiles)
+                                   : dchunk == d_chunk_min<FP8>();
     cnt[i] = cnt_a[i] + (alt ? cnt_d[i] : 0);
-    if (MODE == MODE_PREFILL && r0 + i < p.np && pf_splits(p, r0 + i, tmr[i], sm.pf_split_thr)) cnt[i] *= 2;
+    if (sp) cnt[i] *= 2;
     local_sum += cnt[i];
   }
   int incl = local_sum;
@@ -2277,12 +2307,15 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
             pf_work(p, r, wr, tr);
             sp = pf_splits(p, r, tr, sm.pf_split_thr);
           }
-          // Split items only where the row splits (which implies 16-position
-          // blocks); other items keep the tile loop compiled without the
-          // split's range and merge code.
+          // Split items only where the row splits (32-position blocks, 16 in
+          // the folded instantiation); other items keep the tile loop
+          // compiled without the split's range and merge code.
           const int lr = sorted ? (int)(pf_units[item / per_unit] & 0xffffu) * per_unit + item % per_unit
                                 : item - sm.off[r];
-          if (sp) prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
+          if (sp) {
+            if constexpr (!FOLD) prefill_item<FP8, 2, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
+            else prefill_item<FP8, 1, FOLD, true>(p, sm, stage0, stage1, r, lr, ltid, item, true);
+          }
           else if (bq == 16) prefill_item<FP8, 1, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
           else prefill_item<FP8, 2, FOLD>(p, sm, stage0, stage1, r, lr, ltid);
         } else if constexpr (HAS_PF) {

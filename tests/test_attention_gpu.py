@@ -188,11 +188,15 @@ def test_prefill_rows_split_in_key_halves(device, kv_fp8, phases):
     # prefix at least as long as their chunk, run as pairs of items over the
     # two halves of each block's keys, merged by the second.  First case: two
     # long-prefix rows split beside unsplit lighter and cold rows (odd tile
-    # counts: 4096 + 512 keys end mid-tile for the 16-position blocks).
-    # Second: one row of 1,100 new tokens after 1,100 cached ones, alone.
+    # counts: 4096 + 512 keys end mid-tile).  Second: one row of 1,100 new
+    # tokens after 1,100 cached ones, alone.  Every long row splits in both,
+    # so the blocks keep 32 positions.  Third: a cold row of 1,024 tokens,
+    # as long as a workgroup's share allows but unable to split, beside a
+    # long-prefix row that splits: 16-position blocks and split items.
     from slo_attn import workspace_events
     cases = (Case([], [4096, 0, 2900, 1, 130], [512, 700, 96, 33, 5], seed=12, kv_fp8=kv_fp8),
-             Case([], [1100], [1100], seed=13, kv_fp8=kv_fp8))
+             Case([], [1100], [1100], seed=13, kv_fp8=kv_fp8),
+             Case([], [0, 1024], [1024, 256], seed=14, kv_fp8=kv_fp8))
     for case in cases:
         workspace_events(device)
         (mx, mn), got, _ = _check(case, device, phases)
