@@ -207,10 +207,10 @@ typedef struct slo_paged_attention_args {
    * Lk - Lq of a prefill row read through prefill_tables is new row
    * num_decode + cu_q[r] + j - (Lk - Lq).  The result equals the separate
    * store followed by this launch, bit for bit; no slot written by the launch
-   * may be read through a table by it except as such a new token.  With an
-   * E4M3FN pool and prefill rows in the launch the call makes that order
-   * itself: the store kernel, then the attention launch (two kernels on
-   * `stream`, the same bytes and outputs). */
+   * may be read through a table by it except as such a new token.  Launches
+   * without decode rows, and E4M3FN launches with prefill rows, make that
+   * order themselves: the store kernel, then the attention launch (two
+   * kernels on `stream`, the same bytes and outputs). */
   const int32_t* store_slot_mapping;  /* [num_new_rows] or NULL */
   const void* new_k;
   int64_t new_k_row_stride;

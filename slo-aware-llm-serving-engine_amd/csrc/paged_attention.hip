@@ -2048,9 +2048,10 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // already, and take 32-position blocks, whose tiles cost half the LDS
       // operand reads per query (three 512-token chunks after prefixes
       // 0/2048/512: 65.6 -> 50.9 us; two after 0 and 1,024: 38.0 -> 37.3
-      // us); the other rows take 16 only when one of them is this long.  The
-      // folded instantiation keeps 16 for all (its 32-position split items
-      // would spill registers).
+      // us); the other rows take 16 only when one of them is this long.  (A
+      // folded prefill-only instantiation would keep 16 for all: its
+      // 32-position split items spilled registers; launch_attention runs
+      // prefill-only launches without the KV write.)
       if (FOLD || (int64_t)tunsplit * gridDim.x > 2 * wt) bq = 16;
     }
     // (E4M3FN launches always take full 512-token items: measured 27.0 ->
@@ -2374,10 +2375,9 @@ AttnKernel attn_kernel(bool fold, bool fp8, int mode) {
         paged_attention_kernel<false, MODE_DECODE>},
        {paged_attention_kernel<true, MODE_MIXED>, paged_attention_kernel<true, MODE_PREFILL>,
         paged_attention_kernel<true, MODE_DECODE>}},
-      {{paged_attention_kernel<false, MODE_MIXED, true>, paged_attention_kernel<false, MODE_PREFILL, true>,
-        paged_attention_kernel<false, MODE_DECODE, true>},
-       // E4M3FN launches with prefill rows never carry the KV write
-       // (launch_attention runs the store kernel first).
+      // Prefill-only launches and E4M3FN launches with prefill rows never
+      // carry the KV write (launch_attention runs the store kernel first).
+      {{paged_attention_kernel<false, MODE_MIXED, true>, nullptr, paged_attention_kernel<false, MODE_DECODE, true>},
        {nullptr, nullptr, paged_attention_kernel<true, MODE_DECODE, true>}},
   };
   return table[fold ? 1 : 0][fp8 ? 1 : 0][mode];
@@ -2516,12 +2516,17 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
     }
   }
   const bool store = a->store_slot_mapping != nullptr;
-  // The KV write runs inside the launch except on E4M3FN pools with prefill
-  // rows: there it runs as the store kernel first and the launch reads the
-  // pool (same bytes and outputs; the folded E4M3FN instantiations with
-  // prefill rows spilled registers and measured slower, 108 against 72 us on
-  // 24 decode rows of 256-4096 tokens beside two 512-token chunks).
-  const bool fold = store && !(fp8 && do_pf);
+  // The KV write runs inside launches with decode rows except on E4M3FN
+  // pools with prefill rows; elsewhere it runs as the store kernel first and
+  // the launch reads the pool (same bytes and outputs).  The folded E4M3FN
+  // instantiations with prefill rows spilled registers and measured slower
+  // (108 against 72 us on 24 decode rows of 256-4096 tokens beside two
+  // 512-token chunks); prefill-only launches without the write split their
+  // long rows' keys over 32-position blocks, which the folded instantiation
+  // cannot (three 512-token chunks after prefixes 0/2048/512: 74.7 -> 55.1 us
+  // for the step; four cold rows of 267-1,843 tokens 91.1 -> 90.1 us), while
+  // the mixed launch gains from the fold (65.5 against 70.6 us).
+  const bool fold = store && do_dec && !(fp8 && do_pf);
   if (store) {
     if (fp8 && !(a->store_scale_floor > 0.0f))
       return fail(SLO_ERR_INVALID, "paged_attention: the E4M3FN KV write needs store_scale_floor > 0");

@@ -45,8 +45,10 @@ def forward_mixed(q, k, v, k_cache, v_cache, context, scale, store_fn,
     if not k_cache.numel() or not v_cache.numel():
         raise RuntimeError("mixed forward requires an allocated KV pool")
     # The library's own store runs inside the attention launch when the new
-    # rows are contiguous (same result, one launch less); any other store_fn
-    # runs first.  An E4M3FN pool folds it into pure decode steps only (with at
+    # rows are contiguous and the step has decode rows (same result, one
+    # launch less; a step without decode rows gets the store kernel first from
+    # the same call, so that its long rows can split their keys over
+    # 32-position blocks); any other store_fn runs first.  An E4M3FN pool folds it into pure decode steps only (with at
     # most 8 query heads per kv head): the launch then quantises each decode
     # row's newest token itself (16 rows of 64-1,024 tokens: 25.3 us, against
     # the store kernel and a 24.1 us launch).  With prefill rows the folded
