@@ -368,7 +368,7 @@ __device__ __forceinline__ int pf_blocks_above(const int4& g, int bq, int K) {
   if (g.z <= K || g.x + g.y <= K) return 0;
   const int x = K - g.x;
   if (x < 0) return nb;
-  return max(0, nb - x / bq);
+  return max(0, nb - (x >> (bq == 32 ? 5 : 4)));  // x / bq (bq is 16 or 32)
 }
 
 __device__ __forceinline__ float load_partial(const float* p) {
