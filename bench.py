@@ -7,8 +7,9 @@ prefixes 0 and 1024, 1048 new tokens, 512-page pool.  One step = the
 slot-mapped KV write of the 1048 new tokens + the ragged attention, as
 forward_mixed runs them: with a bf16 pool ONE launch that also writes the new
 K/V (the new tokens are read from their rows), with an E4M3FN pool the store
-kernel and then one attention launch.  (Steps without decode rows, configs 1
-and 2, run the store kernel and then the attention launch on either pool.)
+kernel and then one attention launch.  (Steps without decode rows, the
+prefill-only workloads of --configs, run the store kernel and then the
+attention launch on either pool.)
 
 Every time below comes from HIP-graph replays: a graph holds back-to-back
 launches that rotate over 4 copies of the pool (4 x 512 MiB bf16), so no
