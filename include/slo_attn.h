@@ -178,7 +178,7 @@ typedef struct slo_paged_attention_args {
   int32_t prefill_table_stride;
   int32_t prefill_table_width;
   const void* k;                  /* contiguous bf16 K/V, used iff prefill_tables == NULL */
-  int64_t k_row_stride;
+  int64_t k_row_stride;           /* elements, >= num_kv_heads * 128 */
   const void* v;
   int64_t v_row_stride;
   int32_t num_kv_rows;

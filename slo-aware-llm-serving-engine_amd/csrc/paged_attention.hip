@@ -1507,7 +1507,11 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   typedef __attribute__((address_space(3))) const int lds_int;
   lds_int* pages = (lds_int*)(sm.u.pf.pages);
   // Lane-constant element offsets of this thread's 4 tile rows (row
-  // (tid>>4)+16*it, swizzled 16-byte chunk) from the tile's first key.
+  // 16 wave + 4 it + lane / 16, swizzled 16-byte chunk) from the tile's first
+  // key, lowered by 1024 it bytes: a wavefront's four K (or V) loads of a full
+  // tile fill 4 KiB of LDS and share one M0 write, each adding its 1024 it
+  // as the instruction offset (rows are at least 128 elements apart, checked
+  // on the host, so the offsets stay non-negative).
   const int krow = paged ? p.hkv * HD : (int)p.k_stride;  // row strides < 2^25 elements (checked on the host)
   const int vrow = paged ? p.hkv * HD : (int)p.v_stride;
   // FOLD: elements; otherwise bytes (row strides < 2^25 elements: 63 rows
@@ -1515,9 +1519,9 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
   int kgo[4], vgo[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int row = (tid >> 4) + 16 * it;
-    kgo[it] = (FOLD ? 1 : 2) * (row * krow + 8 * ((tid & 15) ^ (row & 15)));
-    vgo[it] = (FOLD ? 1 : 2) * (row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1)));
+    const int row = 16 * wave + 4 * it + (lane >> 4);
+    kgo[it] = (FOLD ? 1 : 2) * (row * krow + 8 * ((tid & 15) ^ (row & 15)) - 512 * it);
+    vgo[it] = (FOLD ? 1 : 2) * (row * vrow + 8 * ((tid & 15) ^ ((row & 7) << 1)) - 512 * it);
   }
   // Tiles per KV block as a multiplicative inverse (ceil(2^32 / tiles), exact
   // for tile indices below 2^16 and 2 to 2^16 tiles per block; one tile per
@@ -1606,7 +1610,7 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     // Inline-asm DMA: the compiler does not track these loads, so it inserts
     // no wait for them before the current tile's LDS reads (it cannot tell
     // which buffer a DMA writes); the loop waits for them explicitly.
-    const uint32_t kdst = lds_addr((buf ? st1 : st0) + 4 * wave * ROWB);
+    const uint32_t kdst = lds_addr((buf ? st1 : st0) + 16 * wave * ROWB);
     const uint32_t vdst = kdst + TILE_BYTES;
     // Without the folded KV write the tile base goes to SGPRs and each load
     // adds a 32-bit lane offset (four cold 1.1k-token prefill rows: 105 -> 101
@@ -1615,24 +1619,34 @@ __device__ void prefill_item(const Params& p, Smem& sm, uint8_t* st0, uint8_t* s
     const void* kb = FOLD ? nullptr : uniform_ptr(ksrc);
     const void* vb = FOLD ? nullptr : uniform_ptr(vsrc);
     auto dma_k = [&](int it) {
-      if constexpr (FOLD) dma16(ksrc + kgo[it], kdst + 16 * it * ROWB);
-      else dma16_at(kb, (uint32_t)kgo[it], kdst + 16 * it * ROWB);
+      if constexpr (FOLD) dma16(ksrc + kgo[it] + 512 * it, kdst + 4 * it * ROWB);
+      else dma16_at(kb, (uint32_t)(kgo[it] + 1024 * it), kdst + 4 * it * ROWB);
     };
     auto dma_v = [&](int it) {
-      if constexpr (FOLD) dma16(vsrc + vgo[it], vdst + 16 * it * ROWB);
-      else dma16_at(vb, (uint32_t)vgo[it], vdst + 16 * it * ROWB);
+      if constexpr (FOLD) dma16(vsrc + vgo[it] + 512 * it, vdst + 4 * it * ROWB);
+      else dma16_at(vb, (uint32_t)(vgo[it] + 1024 * it), vdst + 4 * it * ROWB);
     };
     if (nv == TT) {  // full tile: DMA only
+      if constexpr (FOLD) {
+        dma16x4(ksrc + kgo[0], ksrc + kgo[1], ksrc + kgo[2], ksrc + kgo[3], kdst);
+        dma16x4(vsrc + vgo[0], vsrc + vgo[1], vsrc + vgo[2], vsrc + vgo[3], vdst);
+      } else if constexpr (!FP8) {
+        dma16x4_at(kb, kgo, kdst);
+        dma16x4_at(vb, vgo, vdst);
+      } else {
+        // (The E4M3FN instantiations, at 256 VGPRs, spilled with the four
+        // offsets live at once.)
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        dma_k(it);
-        dma_v(it);
+        for (int it = 0; it < 4; ++it) {
+          dma_k(it);
+          dma_v(it);
+        }
       }
       return ret;
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int row = (tid >> 4) + 16 * it;
+      const int row = 16 * wave + 4 * it + (lane >> 4);
       if (row < nv) {
         dma_k(it);
         dma_v(it);
@@ -2047,11 +2061,11 @@ __global__ void __launch_bounds__(NT, 2) paged_attention_kernel(Params p) {
       // Rows that split their keys in two (below) halve their longest items
       // already, and take 32-position blocks, whose tiles cost half the LDS
       // operand reads per query (three 512-token chunks after prefixes
-      // 0/2048/512: 65.6 -> 50.9 us; two after 0 and 1,024: 38.0 -> 37.3
-      // us); the other rows take 16 only when one of them is this long.  (A
-      // folded prefill-only instantiation would keep 16 for all: its
-      // 32-position split items spilled registers; launch_attention runs
-      // prefill-only launches without the KV write.)
+      // 0/2048/512: 65.7 -> 51.3 us; two after 0 and 1,024: 38.0 -> 37.8
+      // us); the other rows take 16 only when a row this long cannot split
+      // (tunsplit).  (A folded prefill-only instantiation would keep 16 for
+      // all: its 32-position split items spilled registers; launch_attention
+      // runs prefill-only launches without the KV write.)
       if (FOLD || (int64_t)tunsplit * gridDim.x > 2 * wt) bq = 16;
     }
     // (E4M3FN launches always take full 512-token items: measured 27.0 ->
@@ -2510,9 +2524,11 @@ int launch_attention(const slo_paged_attention_args* a, void* ws, size_t ws_byte
         return fail(SLO_ERR_INVALID, "paged_attention: bad prefill tables");
     } else {
       if (!a->k || !a->v || (a->k_row_stride % 8) || (a->v_row_stride % 8) || a->k_row_stride >= (1 << 25) ||
-          a->v_row_stride >= (1 << 25) ||
+          a->v_row_stride >= (1 << 25) || a->k_row_stride < (int64_t)a->num_kv_heads * HD ||
+          a->v_row_stride < (int64_t)a->num_kv_heads * HD ||
           (reinterpret_cast<uintptr_t>(a->k) % 16) || (reinterpret_cast<uintptr_t>(a->v) % 16))
-        return fail(SLO_ERR_INVALID, "paged_attention: contiguous K/V must be 16-byte aligned bf16 rows");
+        return fail(SLO_ERR_INVALID,
+                    "paged_attention: contiguous K/V must be 16-byte aligned bf16 rows of at least num_kv_heads * 128");
     }
   }
   const bool store = a->store_slot_mapping != nullptr;

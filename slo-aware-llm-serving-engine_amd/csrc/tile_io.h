@@ -103,6 +103,32 @@ __device__ __forceinline__ void dma16_at(const void* base, uint32_t off, uint32_
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
+// Four LDS-DMA loads that fill 4 KiB of LDS from one M0 write: load i lands
+// at lds + 1024 i and reads base + o[i] + 1024 i (the instruction offset is
+// added to the global and the LDS address alike), so the caller passes o[i]
+// already lowered by 1024 i.  One M0 write and one wait state for four loads.
+__device__ __forceinline__ void dma16x4_at(const void* base, const int (&o)[4], uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %5\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %4\n\t"
+      "global_load_lds_dwordx4 %1, %4 offset:1024\n\t"
+      "global_load_lds_dwordx4 %2, %4 offset:2048\n\t"
+      "global_load_lds_dwordx4 %3, %4 offset:3072" ::"v"(o[0]),
+      "v"(o[1]), "v"(o[2]), "v"(o[3]), "s"(base), "s"(lds)
+      : "memory", "m0");
+}
+// The same with 64-bit lane addresses (p_i already lowered by 1024 i bytes).
+__device__ __forceinline__ void dma16x4(const void* p0, const void* p1, const void* p2, const void* p3,
+                                        uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off\n\t"
+      "global_load_lds_dwordx4 %1, off offset:1024\n\t"
+      "global_load_lds_dwordx4 %2, off offset:2048\n\t"
+      "global_load_lds_dwordx4 %3, off offset:3072" ::"v"(p0),
+      "v"(p1), "v"(p2), "v"(p3), "s"(lds)
+      : "memory", "m0");
+}
 // A pointer that is the same in every lane, moved to SGPRs.
 __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   const uint64_t a = (uint64_t)(uintptr_t)p;

@@ -68,6 +68,16 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     args.workspace = 8192
     assert lib.slo_paged_attention(ctypes.byref(args), None) == 4
     assert "block_size" in lib.slo_last_error().decode()
+    # a contiguous prefill row whose K rows are closer than num_kv_heads * 128
+    # elements is refused (the pointers are never dereferenced)
+    cu = (ctypes.c_int32 * 2)(0, 64)
+    args.num_decode, args.num_prefill, args.num_q_rows, args.phases = 0, 1, 64, 3
+    args.prefill_cu_q = args.prefill_cu_k = ctypes.cast(cu, ctypes.c_void_p).value
+    args.k = args.v = 4096
+    args.k_row_stride, args.v_row_stride = 8 * 128 - 8, 8 * 128
+    assert lib.slo_paged_attention(ctypes.byref(args), None) == 1
+    assert "num_kv_heads * 128" in lib.slo_last_error().decode()
+    args.num_prefill, args.num_decode = 0, 1
     # the workspace check refuses a missing or too small workspace before any HIP call
     assert lib.slo_attention_workspace_check(None, 1 << 20, None, None) == 1
     assert lib.slo_attention_workspace_check(8192, 1024, None, None) == 1
