@@ -1,7 +1,7 @@
 """The documented drop-in route for the metadata side channel, on the CPU.
 
-INTEGRATION.md replaces nanovllm/utils/context.py (reference lines 1-28) by a
-re-export of slo_attn.context.  This test writes that module into a scratch
+The drop-in route replaces nanovllm/utils/context.py (reference lines 1-28) by
+a re-export of slo_attn.context.  This test writes that module into a scratch
 ``nanovllm`` package, publishes a step through it as the reference runners do
 (positional ``set_context``, mixed_model_runner.py:71,91 and
 model_runner.py:169,187) and checks that ``slo_attn.Attention`` sees the same
